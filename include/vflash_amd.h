@@ -1,0 +1,179 @@
+/*
+ * vflash_amd: C-ABI of the MI355X (gfx950) quantized-linear path.
+ *
+ * Every entry point enqueues work on the given HIP stream (`stream` is a
+ * hipStream_t; NULL is the legacy default stream) and returns immediately.
+ * None allocates memory, synchronizes, or keeps a pointer after it returns.
+ * All pointers are device pointers owned by the caller.  Element types:
+ *   e4m3  : OCP FP8 E4M3 ("fn": no infinities, max 448), one byte per value
+ *   bf16  : bfloat16, two bytes
+ *   fp32  : IEEE binary32
+ * Strides (ld*) are in elements of the pointed-to type.
+ *
+ * Return value: VFLASH_OK, or a negative status; no work was enqueued when a
+ * negative status is returned.  vflash_status_string() names a status.
+ */
+#ifndef VFLASH_AMD_H
+#define VFLASH_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VFLASH_OK 0
+#define VFLASH_EINVAL (-1)  /* an argument is outside the declared contract */
+#define VFLASH_ELAUNCH (-2) /* the HIP runtime refused the launch */
+
+/* Version of this interface; bumped when a signature changes. */
+int vflash_abi_version(void);
+
+/* Static string for a status code. */
+const char* vflash_status_string(int status);
+
+/*
+ * Per-token E4M3 activation quantization.
+ * Replaces quantize_activation / _rows_fp8
+ *   (src/vflash/native/h3_fp8_activation.py:12-55) and its portable twin
+ *   _quantize_activation_torch (src/vflash/native/h3_fp8_linear.py:18-31).
+ *   x      bf16 [m, k], row stride ldx (>= k), unit column stride
+ *   codes  e4m3 [m_pad, k] contiguous;  scales fp32 [m_pad]
+ *   scale[r] = amax_r > 0 ? max(amax_r / 448, FLT_MIN) : 1
+ *   code     = e4m3_rne(clamp(x / scale[r], -448, 448))
+ *   Rows m..m_pad-1 are padding: codes 0, scale 1.  Requires 1 <= k, m <= m_pad.
+ */
+int vflash_quantize_rows_e4m3(const void* x, int64_t m, int64_t k, int64_t ldx, void* codes,
+                              float* scales, int64_t m_pad, void* stream);
+
+/*
+ * W8A8 linear with per-token and per-output-channel scales and bias.
+ * Replaces the w8a8 branch of RowFP8Execution.linear
+ *   (src/vflash/native/h3_fp8_linear.py:98-121): torch._scaled_mm(codes,
+ *   weight.t(), scale_a, scale_b, out_dtype=bf16) then "+ bias".
+ *   a   e4m3 [m, k] row stride lda;  sa fp32 [m]
+ *   w   e4m3 [n, k] row stride ldw;  sw fp32 [n]
+ *   bias bf16 [n] or NULL;  out bf16 [m, n] row stride ldo
+ *   out = bf16(bf16(sum_k a*w * sa[m] * sw[n]) + bias[n])   (binary32 accumulation)
+ *   Requires k % 16 == 0, n % 16 == 0, lda/ldw % 16 == 0, ldo % 4 == 0 (elements),
+ *   a, w 16-byte aligned; bias, out 8-byte aligned.
+ */
+int vflash_fp8_linear(const void* a, const float* sa, int64_t lda, const void* w,
+                      const float* sw, int64_t ldw, int64_t m, int64_t n, int64_t k,
+                      const void* bias, void* out, int64_t ldo, void* stream);
+
+/*
+ * Merged QKV projection into separate planes.
+ * Replaces the fused to_q/to_k/to_v forward of dense_reference_execution
+ *   (src/vflash/adapters/h3_reference_execution.py:141-192: one linear over
+ *   cat(Wq, Wk, Wv) then .chunk(3, -1)) and the plane copy of tiled_forward
+ *   (src/vflash/native/h3_tiled_block.py:45-60).
+ *   Arithmetic is vflash_fp8_linear's; output column c is written to
+ *   out[(c / plane_cols) * plane_stride + row * ldo + c % plane_cols].
+ *   Requires plane_cols % 16 == 0 and n % plane_cols == 0.
+ */
+int vflash_fp8_linear_planes(const void* a, const float* sa, int64_t lda, const void* w,
+                             const float* sw, int64_t ldw, int64_t m, int64_t n, int64_t k,
+                             const void* bias, void* out, int64_t ldo, int64_t plane_cols,
+                             int64_t plane_stride, void* stream);
+
+/*
+ * FFN up-projection with a GELU-tanh epilogue.
+ * Replaces RowFP8Execution.linear + the FFN activation kernel
+ *   (src/vflash/native/h3_native_denoiser.py:369-382; the reference activation
+ *   is SiLU-mul at src/vflash/native/h3_fused_ops.py:184-224, GELU-tanh is the
+ *   activation of this path's FFN).
+ *   g = bf16(gelu_tanh(bf16(bf16(acc * sa * sw) + bias)))  written to g [m, n] (ldg)
+ *   amax_part fp32 [m, vflash_row_parts(n)]: max |g| of each row over each
+ *   64-column group, consumed by vflash_requant_rows_e4m3.
+ */
+int vflash_fp8_linear_gelu(const void* a, const float* sa, int64_t lda, const void* w,
+                           const float* sw, int64_t ldw, int64_t m, int64_t n, int64_t k,
+                           const void* bias, void* g, int64_t ldg, float* amax_part,
+                           void* stream);
+
+/* Number of 64-column groups per row in amax_part: ceil(n / 64). */
+int64_t vflash_row_parts(int64_t n);
+
+/*
+ * Per-token E4M3 requantization from epilogue row maxima.
+ * Same arithmetic as vflash_quantize_rows_e4m3 (the down projection's own
+ * activation quantization, src/vflash/native/h3_fp8_linear.py:102-108), with
+ * amax taken as the maximum of amax_part[row, 0..parts).
+ *   g bf16 [m, k] (ldg);  codes e4m3 [m_pad, k];  scales fp32 [m_pad]
+ *   Requires k % 8 == 0, ldg % 8 == 0, g 16-byte aligned.
+ */
+int vflash_requant_rows_e4m3(const void* g, int64_t m, int64_t k, int64_t ldg,
+                             const float* amax_part, int64_t parts, void* codes, float* scales,
+                             int64_t m_pad, void* stream);
+
+/*
+ * FFN down-projection with the adaLN gate-residual epilogue.
+ * Replaces RowFP8Execution.linear + triton_strict_bf16_gate_residual
+ *   (src/vflash/native/h3_fused_ops.py:124-170, 614-657).
+ *   y   = bf16(bf16(acc * sa * sw) + bias)
+ *   out = bf16(residual[m, n] + bf16(gate[m * gate_ts + n * gate_hs] * y))
+ *   gate_ts = 0 broadcasts one gate row over all tokens.  out may alias residual
+ *   only when ldo == ldr.
+ */
+int vflash_fp8_linear_gate_residual(const void* a, const float* sa, int64_t lda, const void* w,
+                                    const float* sw, int64_t ldw, int64_t m, int64_t n,
+                                    int64_t k, const void* bias, const void* gate,
+                                    int64_t gate_ts, int64_t gate_hs, const void* residual,
+                                    int64_t ldr, void* out, int64_t ldo, void* stream);
+
+/*
+ * LoRA down-projection t = bf16(x . A^T) (binary32 accumulation).
+ * Replaces the inner F.linear of the activation-adapter hook
+ *   (src/vflash/adapters/h3_reference_lora.py:80-82).
+ *   x bf16 [m, k] (ldx);  lora_a bf16 [rank, k] contiguous;  t bf16 [m, rank] contiguous
+ *   Requires rank % 16 == 0, rank <= 128, k % 16 == 0, ldx % 8 == 0.
+ */
+int vflash_lora_down(const void* x, int64_t m, int64_t k, int64_t ldx, const void* lora_a,
+                     int64_t rank, void* t, void* stream);
+
+/*
+ * W8A8 linear with a fused LoRA up-projection and merge.
+ * Replaces the outer F.linear and merge of the adapter hook
+ *   (src/vflash/adapters/h3_reference_lora.py:80-90):
+ *   base  = vflash_fp8_linear's output
+ *   delta = bf16(t . B^T); if scale != 1: bf16(delta * scale);
+ *           if strength != 1: bf16(delta * strength)
+ *   out   = bf16(base + delta)
+ *   t bf16 [m, rank] (ldt);  lora_b bf16 [n, rank] (ldb);  rank % 16 == 0, <= 128.
+ */
+int vflash_fp8_linear_lora(const void* a, const float* sa, int64_t lda, const void* w,
+                           const float* sw, int64_t ldw, int64_t m, int64_t n, int64_t k,
+                           const void* bias, const void* t, int64_t ldt, const void* lora_b,
+                           int64_t ldb, int64_t rank, float scale, float strength, void* out,
+                           int64_t ldo, void* stream);
+
+/*
+ * NVFP4-weight linear (W4A8: E4M3 per-token activations, E2M1 weights with
+ * E4M3 scales per 16-element K block and an fp32 output multiplier).
+ * Replaces the mm_fp4 call of NVFP4Execution.linear
+ *   (src/vflash/native/h3_nvfp4_linear.py:118-139).
+ *   a        e4m3 [m, k] (lda);  sa fp32 [m]
+ *   w_packed u8 [n, k/2]: element 2j in the low nibble, 2j+1 in the high nibble
+ *   w_scales u8 (e4m3) [n, k/16] in the 128x4 tiled order of NVFP4Weight
+ *            (h3_nvfp4_linear.py:22-33)
+ *   alpha    fp32 device scalar (NVFP4Weight.alpha; read on the device, no host sync)
+ *   out = bf16(bf16(sum_k a * e2m1(w) * e4m3(s_blk) * sa[m] * alpha) + bias[n])
+ *   Requires n % 128 == 0, k % 64 == 0.
+ */
+int vflash_nvfp4_linear(const void* a, const float* sa, int64_t lda, const void* w_packed,
+                        const void* w_scales, const float* alpha, int64_t m, int64_t n, int64_t k,
+                        const void* bias, void* out, int64_t ldo, void* stream);
+
+/*
+ * Tuning hook: force a GEMM tile configuration for later calls in this process
+ * (0 = automatic, 1 = 256x256, 2 = 128x128, 3 = 64x64, 4 = 128x256, 5 = 256x128)
+ * and the tile-order group height (0 = default).  Returns the previous tile value.
+ */
+int vflash_set_gemm_tile(int tile, int group_m);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VFLASH_AMD_H */

@@ -1,0 +1,123 @@
+"""W8A8 path restated on the CPU in numpy (test infrastructure).
+
+Inputs and outputs are numpy arrays; bf16 tensors are carried as binary32
+arrays holding bf16-representable values.  Elementwise steps use binary32
+arithmetic with a bf16 rounding after each step, as the reference's kernels
+do; the GEMM sum is exact (binary64 sums of E4M3 products are exact at these
+sizes) and rounded once to bf16 after the two scales.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from oracle.formats import FLT_MIN, bf16_round, e4m3_decode, e4m3_encode
+
+F32 = np.float32
+
+
+def quantize_rows(x, pad: int = 16):
+    """Per-token E4M3 codes and scales with GEMM row padding.
+
+    Follows src/vflash/native/h3_fp8_linear.py:18-31 (and the fused kernel
+    h3_fp8_activation.py:12-28): binary32 row maximum;
+    scale = max(amax / 448, FLT_MIN) if amax > 0 else 1 (IEEE binary32
+    division); codes = e4m3(clamp(x / scale, -448, 448)); rows padded to a
+    multiple of ``pad`` with codes 0 and scale 1.
+    Pinned by: the reference KATs (tests/test_fp8_linear.py:99-120, restated in
+    tests/golden), torch's float8_e4m3fn cast, and closed-form invariants.
+    """
+    x = np.asarray(x, dtype=F32)
+    m, k = x.shape
+    m_pad = -(-m // pad) * pad if pad > 1 else m
+    amax = np.max(np.abs(x), axis=1) if k else np.zeros(m, F32)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        scale = np.where(amax > 0, np.maximum(amax / F32(448.0), FLT_MIN), F32(1.0)).astype(F32)
+        q = np.clip(x / scale[:, None], F32(-448.0), F32(448.0))
+    codes = np.zeros((m_pad, k), dtype=np.uint8)
+    codes[:m] = e4m3_encode(q)
+    scales = np.ones(m_pad, dtype=F32)
+    scales[:m] = scale
+    return codes, scales
+
+
+def gemm_acc(a_codes, w_codes) -> np.ndarray:
+    """Exact sum_k a[m,k] * w[n,k] of E4M3 values (binary64)."""
+    a = e4m3_decode(a_codes).astype(np.float64)
+    w = e4m3_decode(w_codes).astype(np.float64)
+    return a @ w.T
+
+
+def scaled_mm(a_codes, sa, w_codes, sw) -> np.ndarray:
+    """bf16(acc * sa[m] * sw[n]): the _scaled_mm call of h3_fp8_linear.py:110-117.
+
+    The scale products are formed in binary64 and rounded once to bf16; the
+    reference library's binary32 epilogue order is not observable here, so
+    kernel outputs are compared to this within a relative tolerance.
+    """
+    acc = gemm_acc(a_codes, w_codes)
+    sa = np.asarray(sa, dtype=np.float64).reshape(-1, 1)
+    sw = np.asarray(sw, dtype=np.float64).reshape(1, -1)
+    return bf16_round(acc * sa[: acc.shape[0]] * sw)
+
+
+def add_bias(y, bias) -> np.ndarray:
+    """The second rounding: bf16(y + bias) in binary32 (h3_fp8_linear.py:121)."""
+    if bias is None:
+        return np.asarray(y, dtype=F32)
+    return bf16_round(np.asarray(y, F32) + np.asarray(bias, F32).reshape(1, -1))
+
+
+def w8a8_linear(x, w_codes, sw, bias=None):
+    """RowFP8Execution.linear in w8a8 mode (h3_fp8_linear.py:98-121) for a 2-D input."""
+    codes, sa = quantize_rows(x)
+    m = np.asarray(x).shape[0]
+    return add_bias(scaled_mm(codes[:m], sa[:m], w_codes, sw), bias)
+
+
+def gelu_tanh(y) -> np.ndarray:
+    """bf16(0.5 y (1 + tanh(sqrt(2/pi) (y + 0.044715 y^3)))) in binary32.
+
+    The reference has no GELU (its FFN is SiLU-mul); this is the textbook tanh
+    approximation, pinned against torch.nn.functional.gelu(approximate="tanh").
+    """
+    y = np.asarray(y, dtype=F32)
+    beta = F32(0.7978845608028654)
+    kappa = F32(0.044715)
+    inner = beta * (y + kappa * y * y * y)
+    return bf16_round(F32(0.5) * y * (F32(1.0) + np.tanh(inner)))
+
+
+def gate_residual(residual, gate, y) -> np.ndarray:
+    """bf16(residual + bf16(gate * y)) in binary32 (h3_fused_ops.py:153-170)."""
+    gated = bf16_round(np.asarray(gate, F32) * np.asarray(y, F32))
+    return bf16_round(np.asarray(residual, F32) + gated)
+
+
+def lora_delta(x, lora_a, lora_b, scaling: float = 1.0, strength: float = 1.0):
+    """The adapter hook's delta (src/vflash/adapters/h3_reference_lora.py:80-89):
+    t = bf16(x A^T); d = bf16(t B^T); bf16(d * scaling) if scaling != 1;
+    bf16(d * strength) if strength != 1.  Sums exact in binary64."""
+    t = bf16_round(np.asarray(x, np.float64) @ np.asarray(lora_a, np.float64).T)
+    d = bf16_round(t.astype(np.float64) @ np.asarray(lora_b, np.float64).T)
+    if scaling != 1.0:
+        d = bf16_round(d * F32(scaling))
+    if strength != 1.0:
+        d = bf16_round(d * F32(strength))
+    return d
+
+
+def lora_merge(base, delta) -> np.ndarray:
+    """bf16(result + delta) (h3_reference_lora.py:90)."""
+    return bf16_round(np.asarray(base, F32) + np.asarray(delta, F32))
+
+
+def ffn(x, up_codes, up_scale, up_bias, down_codes, down_scale, down_bias, gate, residual):
+    """The FFN chain of this path: up + bias, GELU-tanh, per-token requant,
+    down + bias, gate-residual.  Returns (g, h_codes, h_scales, out)."""
+    x = np.asarray(x, F32)
+    m = x.shape[0]
+    g = gelu_tanh(w8a8_linear(x, up_codes, up_scale, up_bias))
+    h_codes, h_scales = quantize_rows(g)
+    y = add_bias(scaled_mm(h_codes[:m], h_scales[:m], down_codes, down_scale), down_bias)
+    return g, h_codes, h_scales, gate_residual(residual, gate, y)

@@ -1,0 +1,76 @@
+"""The C-ABI library loads and exports every symbol include/vflash_amd.h declares.
+
+CPU-only: no entry point that launches a kernel is called; argument checks
+that fail before any launch are exercised (no work is enqueued on EINVAL).
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from vflash_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "vflash_amd.h"
+
+
+def declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(vflash_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_path():
+    names = declared()
+    for must in (
+        "vflash_quantize_rows_e4m3",
+        "vflash_fp8_linear",
+        "vflash_fp8_linear_planes",
+        "vflash_fp8_linear_gelu",
+        "vflash_requant_rows_e4m3",
+        "vflash_fp8_linear_gate_residual",
+        "vflash_lora_down",
+        "vflash_fp8_linear_lora",
+        "vflash_nvfp4_linear",
+    ):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.library()
+    for name in declared():
+        assert hasattr(lib, name), name
+    assert set(declared()) == set(_lib.SIGNATURES)
+
+
+def test_status_strings_and_version():
+    lib = _lib.library()
+    assert lib.vflash_abi_version() == 1
+    assert lib.vflash_status_string(_lib.VFLASH_EINVAL) == b"argument outside the declared contract"
+    assert lib.vflash_row_parts(13824) == 216 and lib.vflash_row_parts(64) == 1
+
+
+@pytest.mark.parametrize(
+    "args",
+    [
+        # null operands, k % 16, n % 16, lda < k: rejected before any launch
+        (None, None, 64, None, None, 64, 1, 16, 64, None, None, 16, None),
+        (16, 16, 64, 16, 16, 64, 1, 16, 24, None, 16, 16, None),
+        (16, 16, 64, 16, 16, 64, 1, 24, 64, None, 16, 24, None),
+        (16, 16, 32, 16, 16, 64, 1, 16, 64, None, 16, 16, None),
+    ],
+)
+def test_contract_violations_return_einval_without_launching(args):
+    lib = _lib.library()
+    conv = [ctypes.c_void_p(a) if i in (0, 1, 3, 4, 9, 10, 12) and a is not None else a
+            for i, a in enumerate(args)]
+    assert lib.vflash_fp8_linear(*conv) == _lib.VFLASH_EINVAL
+
+
+def test_nvfp4_and_lora_contracts():
+    lib = _lib.library()
+    p = ctypes.c_void_p(256)
+    # n not a multiple of 128
+    assert lib.vflash_nvfp4_linear(p, p, 64, p, p, p, 1, 64, 64, None, p, 64, None) == -1
+    # rank not a multiple of 16
+    assert lib.vflash_lora_down(p, 4, 64, 64, p, 20, p, None) == -1

@@ -1,0 +1,128 @@
+"""W8A8 linear on gfx950 against the oracle (bf16 outputs within 1e-2 relative)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8 as O
+from tests.conftest import golden, rel_check
+from vflash_amd import _lib, kernels
+from vflash_amd.fp8_linear import RowFP8Execution, RowFP8Linear
+from vflash_amd.prepare import quantize_weight_rows
+
+pytestmark = pytest.mark.gpu
+
+TILES = [1, 2, 3, 4, 5]
+
+
+@pytest.fixture
+def tile():
+    yield
+    _lib.set_gemm_tile(0)
+
+
+def seeded(m, k, n, bias=True, seed=0):
+    """BASELINE input recipe: fp32 draws on CPU in the order X, W, bias, then casts."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((m, k), generator=g).to(torch.bfloat16)
+    w = torch.randn((n, k), generator=g) * 0.02
+    b = (torch.randn(n, generator=g) * 0.01).to(torch.bfloat16) if bias else None
+    codes, scale = quantize_weight_rows(w)
+    return x, codes, scale, b
+
+
+def oracle_linear(x, codes, scale, b, rows=None):
+    xs = x.float().numpy() if rows is None else x.float().numpy()[rows]
+    return O.w8a8_linear(
+        xs,
+        codes.view(torch.uint8).numpy(),
+        scale.reshape(-1).numpy(),
+        None if b is None else b.float().numpy(),
+    )
+
+
+def test_golden_small_case_through_the_c_abi(dev):
+    g = golden("gemm_small.npz")
+    m = g["x"].shape[0]
+    a = torch.from_numpy(g["a_codes"]).view(torch.float8_e4m3fn).to(dev)
+    sa = torch.from_numpy(g["sa"]).to(dev)
+    w = torch.from_numpy(g["w_codes"]).view(torch.float8_e4m3fn).to(dev)
+    sw = torch.from_numpy(g["sw"]).to(dev)
+    bias = torch.from_numpy(g["bias"]).to(torch.bfloat16).to(dev)
+    out = kernels.fp8_gemm(a, sa, w, sw, m, bias).float().cpu().numpy()
+    _, exact = rel_check(out, g["expected"])
+    assert exact > 0.95  # the exact-sum reference differs only by rare ties of fp32 sums
+    nob = kernels.fp8_gemm(a, sa, w, sw, m).float().cpu().numpy()
+    rel_check(nob, g["scaled"])
+
+
+def test_baseline_config_small_linear(dev):
+    # X bf16 [4096, 3072] N(0,1); W N(0, 0.02) -> e4m3 [3072, 3072]; bias N(0, 0.01); seed 0.
+    x, codes, scale, b = seeded(4096, 3072, 3072)
+    ex = RowFP8Execution("w8a8", activation_quantizer="triton")
+    out = ex.linear(x.to(dev), codes.to(dev), scale.to(dev), b.to(dev))
+    assert out.dtype == torch.bfloat16 and out.shape == (4096, 3072)
+    worst, exact = rel_check(out.float().cpu().numpy(), oracle_linear(x, codes, scale, b))
+    assert exact > 0.9
+    assert ex.calls == {"weight_only": 0, "w8a8": 1}
+
+
+@pytest.mark.parametrize("cfg", TILES)
+@pytest.mark.parametrize("m,k,n", [(1, 16, 16), (17, 48, 272), (300, 144, 48), (257, 256, 528)])
+def test_edges_under_every_tile_configuration(dev, tile, cfg, m, k, n):
+    _lib.set_gemm_tile(cfg)
+    x, codes, scale, b = seeded(m, k, n, seed=m + k + n)
+    codes_d, scale_d = codes.to(dev), scale.to(dev)
+    a, sa = kernels.quantize_rows(x.to(dev))
+    out = kernels.fp8_gemm(a, sa, codes_d, scale_d, m, b.to(dev))
+    rel_check(out.float().cpu().numpy(), oracle_linear(x, codes, scale, b))
+    out = kernels.fp8_gemm(a, sa, codes_d, scale_d, m, None)
+    rel_check(out.float().cpu().numpy(), oracle_linear(x, codes, scale, None))
+
+
+def test_three_dimensional_input_and_torch_quantizer(dev):
+    x, codes, scale, b = seeded(2 * 3 * 40, 256, 64)
+    x3 = x.reshape(2, 120, 256)
+    ex = RowFP8Execution("w8a8", activation_quantizer="torch")
+    out = ex.linear(x3.to(dev), codes.to(dev), scale.to(dev), b.to(dev))
+    assert out.shape == (2, 120, 64)
+    rel_check(out.reshape(-1, 64).float().cpu().numpy(), oracle_linear(x, codes, scale, b))
+
+
+def test_module_forward_and_measure_scopes(dev):
+    x, codes, scale, b = seeded(64, 128, 32)
+    scopes = []
+
+    class Scope:
+        def __init__(self, name):
+            self.name = name
+
+        def __enter__(self):
+            scopes.append(self.name)
+
+        def __exit__(self, *exc):
+            return False
+
+    ex = RowFP8Execution("w8a8", activation_quantizer="triton", measure=Scope)
+    original = torch.nn.Linear(128, 32, dtype=torch.bfloat16)
+    original.bias.data.copy_(b)
+    module = RowFP8Linear(original, ex)
+    module.load_state_dict(
+        {"weight": codes.to(dev), "row_scale": scale.to(dev), "bias": original.bias.to(dev)},
+        assign=True,
+    )
+    out = module(x.to(dev))
+    rel_check(out.float().cpu().numpy(), oracle_linear(x, codes, scale, b))
+    assert scopes == ["linear.activation_quantize", "linear.fp8_gemm"]
+
+
+def test_metric_shape_sampled_rows(dev):
+    # M=32760, K=5120, N=13824: every row is computed, sampled rows are checked,
+    # including the 248-row partial last tile.
+    x, codes, scale, b = seeded(32760, 5120, 13824)
+    ex = RowFP8Execution("w8a8", activation_quantizer="triton")
+    out = ex.linear(x.to(dev), codes.to(dev), scale.to(dev), b.to(dev))
+    rows = np.r_[0:32, 4096:4128, 32512:32520, 32728:32760]
+    got = out.float().cpu().numpy()[rows]
+    rel_check(got, oracle_linear(x, codes, scale, b, rows=rows))
+    assert bool(torch.isfinite(out.float()).all())

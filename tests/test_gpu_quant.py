@@ -1,0 +1,133 @@
+"""Per-token E4M3 quantization on gfx950: bit-exact against the oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8 as O
+from oracle.formats import bf16_from_bits
+from tests.conftest import golden
+from vflash_amd import kernels
+from vflash_amd.fp8_activation import quantize_activation
+from vflash_amd.fp8_linear import _quantize_activation_torch
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu_quant(x_np, dev, ldx=None):
+    x = torch.from_numpy(np.ascontiguousarray(x_np, np.float32)).to(torch.bfloat16)
+    if ldx is not None:
+        big = torch.full((x.shape[0], ldx), float("nan"), dtype=torch.bfloat16)
+        big[:, : x.shape[1]] = x
+        x = big.to(dev)[:, : x_np.shape[1]]
+    else:
+        x = x.to(dev)
+    codes, scales = kernels.quantize_rows(x)
+    torch.cuda.synchronize()
+    return codes.view(torch.uint8).cpu().numpy(), scales.reshape(-1).cpu().numpy(), x
+
+
+def assert_exact(x_np, dev, **kw):
+    codes, scales, _ = gpu_quant(x_np, dev, **kw)
+    ref_codes, ref_scales = O.quantize_rows(x_np)
+    assert np.array_equal(scales.view(np.uint32), ref_scales.view(np.uint32)), "scales differ"
+    bad = codes != ref_codes
+    assert not bad.any(), f"{bad.sum()} codes differ, first at {np.argwhere(bad)[:3]}"
+
+
+@pytest.mark.parametrize("rows", [1, 16, 17])
+def test_reference_kat_rows(dev, rows):
+    g = golden("quant_kat.npz")
+    codes, scales, _ = gpu_quant(g[f"x{rows}"], dev)
+    assert np.array_equal(codes, g[f"codes{rows}"]) and np.array_equal(scales, g[f"scales{rows}"])
+
+
+def test_random_rows_over_60_decades(dev):
+    g = golden("quant_kat.npz")
+    codes, scales, _ = gpu_quant(g["xr"], dev)
+    assert np.array_equal(codes, g["codesr"]) and np.array_equal(scales, g["scalesr"])
+
+
+def test_every_bf16_bit_pattern_under_many_scales(dev):
+    v = bf16_from_bits(np.arange(65536, dtype=np.uint32).astype(np.uint16))
+    v = v[np.isfinite(v)]
+    rng = np.random.default_rng(0)
+    v = v[rng.permutation(v.size)]
+    k = 256
+    n = v.size // k * k
+    x = v[:n].reshape(-1, k)  # each row gets its own amax (and so its own scale)
+    assert_exact(x, dev)
+    # Rows whose maximum is tiny: scale hits the FLT_MIN floor, subnormal inputs.
+    tiny = bf16_from_bits(np.arange(1, 0x0100, dtype=np.uint16))
+    assert_exact(np.stack([tiny[:128], -tiny[:128], tiny[-128:]]), dev)
+
+
+@pytest.mark.parametrize("k", [16, 64, 3072, 5120, 13824, 16384])
+def test_aligned_widths_exact(dev, k):
+    rng = np.random.default_rng(k)
+    x = rng.standard_normal((67, k)).astype(np.float32) * rng.uniform(0.01, 100, (67, 1))
+    x[5] = 0.0
+    assert_exact(x, dev)
+
+
+@pytest.mark.parametrize("k", [17, 100, 1000, 20000, 32768])
+def test_generic_widths_exact(dev, k):
+    rng = np.random.default_rng(k)
+    x = rng.standard_normal((9, k)).astype(np.float32) * 3
+    assert_exact(x, dev)
+
+
+def test_strided_input_is_read_not_written(dev):
+    # The FFN value half of [M, 2F] has a doubled row stride (test_fp8_linear.py:99-115).
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((33, 512)).astype(np.float32)
+    codes, scales, view = gpu_quant(x, dev, ldx=1024)
+    ref_codes, ref_scales = O.quantize_rows(x)
+    assert np.array_equal(codes, ref_codes) and np.array_equal(scales, ref_scales)
+    base = view.as_strided((33, 1024), (1024, 1))
+    assert torch.isnan(base[:, 512:].float()).all()
+
+
+def test_matches_portable_torch_expression_on_device(dev):
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn((4096, 3072), generator=g).to(torch.bfloat16).to(dev)
+    c1, s1 = quantize_activation(x)
+    c2, s2 = _quantize_activation_torch(x)
+    assert torch.equal(c1.view(torch.uint8), c2.view(torch.uint8)) and torch.equal(s1, s2)
+
+
+def test_metric_shape_sampled_rows_and_full_properties(dev):
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn((32760, 5120), generator=g).to(torch.bfloat16)
+    codes, scales = kernels.quantize_rows(x.to(dev))
+    assert codes.shape == (32768, 5120)
+    # Every element: dequantized value within half an E4M3 step of the input.
+    xd = x.to(dev).float()
+    dq = codes[:32760].float() * scales[:32760]
+    q = (xd / scales[:32760]).abs()
+    step = torch.where(q < 2.0**-6, torch.full_like(q, 2.0**-9), torch.exp2(torch.floor(torch.log2(q.clamp_min(1e-30))) - 3))
+    assert bool(((dq - xd).abs() <= 0.5 * step * scales[:32760] * (1 + 1e-6)).all())
+    assert bool((codes[32760:].view(torch.uint8) == 0).all()) and bool((scales[32760:] == 1).all())
+    rows = np.r_[0:64, 16000:16064, 32696:32760]
+    c = codes.view(torch.uint8).cpu().numpy()[rows]
+    s = scales.reshape(-1).cpu().numpy()[rows]
+    rc, rs = O.quantize_rows(x.float().numpy()[rows], pad=1)
+    assert np.array_equal(c, rc) and np.array_equal(s, rs)
+
+
+def test_row_offsets_beyond_2_pow_31_elements(dev):
+    # Strided rows whose byte offset crosses 2^31 (test_fp8_compile.py:16-40 shape).
+    k = 14336
+    stride = 2 * k
+    m = (2**31 + stride - 1) // stride + 17
+    assert (m - 1) * stride > 2**31
+    base = torch.zeros((m, stride), dtype=torch.bfloat16, device=dev)
+    g = torch.Generator().manual_seed(1)
+    tail = torch.randn((40, k), generator=g).to(torch.bfloat16)
+    base[m - 40 :, :k] = tail.to(dev)
+    codes, scales = kernels.quantize_rows(base[:, :k])
+    c = codes[m - 40 : m].view(torch.uint8).cpu().numpy()
+    s = scales[m - 40 : m].reshape(-1).cpu().numpy()
+    rc, rs = O.quantize_rows(tail.float().numpy(), pad=1)
+    assert np.array_equal(c, rc) and np.array_equal(s, rs)
+    assert bool((scales[: m - 40] == 1).all())

@@ -1,0 +1,137 @@
+"""Pin the W8A8 oracle against the reference's KATs, torch, and exact arithmetic."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8 as O
+from oracle.baseline import weight_only_linear
+from oracle.formats import FLT_MIN, bf16_round, e4m3_decode
+from tests.conftest import golden
+
+
+@pytest.mark.parametrize("rows", [1, 16, 17])
+def test_quant_reference_kat_rows(rows):
+    # tests/test_fp8_linear.py:99-120: zero row -> scale 1, codes 0; tiny row ->
+    # FLT_MIN floor; padding rows zero / 1; codes finite.
+    g = golden("quant_kat.npz")
+    codes, scales = O.quantize_rows(g[f"x{rows}"])
+    padded = (rows + 15) // 16 * 16
+    assert codes.shape == (padded, 64) and scales.shape == (padded,)
+    assert np.array_equal(codes, g[f"codes{rows}"])
+    assert np.array_equal(scales, g[f"scales{rows}"])
+    assert np.all(e4m3_decode(codes[0]) == 0) and scales[0] == 1
+    assert np.all(codes[rows:] == 0) and np.all(scales[rows:] == 1)
+    if rows > 1:
+        assert scales[1] == FLT_MIN
+    x = g[f"x{rows}"]
+    expected = np.maximum(np.abs(x).max(axis=1) / np.float32(448), FLT_MIN)
+    expected[0] = 1
+    assert np.array_equal(scales[:rows], expected.astype(np.float32))
+
+
+def test_quant_random_rows_match_torch_expression_over_60_decades():
+    g = golden("quant_kat.npz")
+    codes, scales = O.quantize_rows(g["xr"])
+    assert np.array_equal(codes, g["codesr"]) and np.array_equal(scales, g["scalesr"])
+
+
+def test_quant_invariants_on_random_rows():
+    rng = np.random.default_rng(3)
+    x = bf16_round(rng.standard_normal((64, 333)) * 10.0 ** rng.uniform(-20, 20, (64, 1)))
+    codes, scales = O.quantize_rows(x)
+    dq = e4m3_decode(codes[:64]).astype(np.float64) * scales[:64, None]
+    # The row maximum maps to +-448 exactly (code 0x7e / 0xfe).
+    arg = np.argmax(np.abs(x), axis=1)
+    assert np.all((codes[np.arange(64), arg] & 0x7F) == 0x7E)
+    # Dequantized values are within half an E4M3 step of the input.
+    q = np.abs(x / scales[:64, None])
+    step = np.where(q < 2.0**-6, 2.0**-9, 2.0 ** (np.floor(np.log2(np.maximum(q, 1e-30))) - 3))
+    assert np.all(np.abs(dq - x) <= 0.5 * step * scales[:64, None] * (1 + 1e-6))
+
+
+def test_gemm_oracle_matches_exact_rational_arithmetic():
+    g = golden("gemm_small.npz")
+    m = g["x"].shape[0]
+    codes, sa = O.quantize_rows(g["x"])
+    assert np.array_equal(codes, g["a_codes"]) and np.array_equal(sa, g["sa"])
+    scaled = O.scaled_mm(codes[:m], sa[:m], g["w_codes"], g["sw"])
+    assert np.array_equal(scaled, g["scaled"])
+    out = O.add_bias(scaled, g["bias"])
+    assert np.array_equal(out, g["expected"])
+    assert np.array_equal(O.w8a8_linear(g["x"], g["w_codes"], g["sw"], g["bias"]), g["expected"])
+
+
+def test_gemm_oracle_detects_a_transposed_or_dropped_scale():
+    g = golden("gemm_small.npz")
+    m = g["x"].shape[0]
+    right = O.scaled_mm(g["a_codes"][:m], g["sa"][:m], g["w_codes"], g["sw"])
+    wrong = O.scaled_mm(g["a_codes"][:m], np.ones(m, np.float32), g["w_codes"], g["sw"])
+    assert not np.array_equal(right, wrong)
+
+
+def test_weight_only_baseline_is_the_reference_expression():
+    g = golden("weight_only_kat.npz")
+    codes = torch.from_numpy(g["codes"]).view(torch.float8_e4m3fn)
+    out = weight_only_linear(
+        torch.from_numpy(g["values"]).to(torch.bfloat16),
+        codes,
+        torch.from_numpy(g["scales"]),
+        torch.from_numpy(g["bias"]).to(torch.bfloat16),
+    )
+    assert np.array_equal(out.float().numpy(), g["expected"])
+
+
+def test_weight_only_loader_kat_ones():
+    # tests/test_fp8_loaders.py:39-47: ones codes x ones scales, ones input -> 16.
+    codes = torch.ones(4, 16).to(torch.float8_e4m3fn)
+    out = weight_only_linear(torch.ones(2, 16), codes, torch.ones(4, 1))
+    assert torch.equal(out, torch.full((2, 4), 16.0))
+
+
+def test_lora_oracle_matches_reference_kat():
+    g = golden("lora_kat.npz")
+    for strength, expected in zip(g["strengths"], g["expected"]):
+        d = O.lora_delta(g["sample"], g["a"], g["b"], 1.0, float(strength))
+        assert np.array_equal(O.lora_merge(g["sample"], d), expected)
+
+
+def test_gelu_oracle_tracks_torch_on_every_bf16_value():
+    from oracle.formats import bf16_from_bits
+
+    x = bf16_from_bits(np.arange(65536, dtype=np.uint32).astype(np.uint16))
+    x = x[np.isfinite(x) & (np.abs(x) < 1e4)]
+    ours = O.gelu_tanh(x)
+    ref = torch.nn.functional.gelu(torch.from_numpy(x).to(torch.bfloat16), approximate="tanh")
+    ref = ref.float().numpy()
+    diff = ours != ref
+    # Different binary32 tanh implementations may flip a bf16 rounding: at most
+    # one bf16 step, or, where 1 + tanh cancels (x << 0), a few binary32 ulps of
+    # tanh scaled by 0.5 |x|.
+    step = np.abs(ref) * 2.0**-7 + np.abs(x) * 2.0**-21 + 2.0**-133
+    assert np.all(np.abs(ours - ref) <= step)
+    assert diff.mean() < 2e-3
+    # Closed forms: gelu(0) = 0, gelu(x) -> x for large x, -> -0 for large -x.
+    assert O.gelu_tanh(np.float32([0.0]))[0] == 0
+    assert O.gelu_tanh(np.float32([30.0]))[0] == 30.0
+    assert O.gelu_tanh(np.float32([-30.0]))[0] == 0
+
+
+def test_gate_residual_matches_torch_eager_bf16():
+    rng = np.random.default_rng(5)
+    res = bf16_round(rng.standard_normal((33, 70)))
+    gate = bf16_round(rng.uniform(0, 1, 70))
+    y = bf16_round(rng.standard_normal((33, 70)) * 3)
+    t = lambda a: torch.from_numpy(np.asarray(a, np.float32)).to(torch.bfloat16)
+    ref = (t(res) + t(gate) * t(y)).float().numpy()
+    assert np.array_equal(O.gate_residual(res, gate, y), ref)
+
+
+def test_merged_qkv_equals_concatenated_projections():
+    rng = np.random.default_rng(6)
+    x = bf16_round(rng.standard_normal((20, 64)))
+    ws = [rng.integers(0, 256, (32, 64)).astype(np.uint8) & 0xF7 for _ in range(3)]
+    ss = [rng.uniform(0.001, 0.01, 32).astype(np.float32) for _ in range(3)]
+    merged = O.w8a8_linear(x, np.concatenate(ws), np.concatenate(ss))
+    parts = [O.w8a8_linear(x, w, s) for w, s in zip(ws, ss)]
+    assert np.array_equal(merged, np.concatenate(parts, axis=1))

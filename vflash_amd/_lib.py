@@ -1,0 +1,114 @@
+"""ctypes binding of libvflash_amd.so (the C-ABI in include/vflash_amd.h).
+
+The library is loaded lazily on first use.  There is no fallback: a missing
+library or a device other than gfx950 raises, so no caller can silently run
+another arithmetic.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from functools import cache
+from pathlib import Path
+
+import torch
+
+LIBRARY = Path(__file__).resolve().with_name("libvflash_amd.so")
+
+VFLASH_OK = 0
+VFLASH_EINVAL = -1
+VFLASH_ELAUNCH = -2
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int
+_F32 = ctypes.c_float
+
+# Signatures of every exported entry point (argument types, return type).
+SIGNATURES: dict[str, tuple[list, object]] = {
+    "vflash_abi_version": ([], _I32),
+    "vflash_status_string": ([_I32], ctypes.c_char_p),
+    "vflash_set_gemm_tile": ([_I32, _I32], _I32),
+    "vflash_quantize_rows_e4m3": ([_P, _I64, _I64, _I64, _P, _P, _I64, _P], _I32),
+    "vflash_fp8_linear": ([_P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P], _I32),
+    "vflash_fp8_linear_planes": (
+        [_P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _P],
+        _I32,
+    ),
+    "vflash_fp8_linear_gelu": (
+        [_P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _P],
+        _I32,
+    ),
+    "vflash_row_parts": ([_I64], _I64),
+    "vflash_requant_rows_e4m3": ([_P, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P], _I32),
+    "vflash_fp8_linear_gate_residual": (
+        [_P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _I64, _P],
+        _I32,
+    ),
+    "vflash_lora_down": ([_P, _I64, _I64, _I64, _P, _I64, _P, _P], _I32),
+    "vflash_fp8_linear_lora": (
+        [_P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _I64, _F32, _F32,
+         _P, _I64, _P],
+        _I32,
+    ),
+    "vflash_nvfp4_linear": (
+        [_P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _P],
+        _I32,
+    ),
+}
+
+
+class KernelError(RuntimeError):
+    """The HIP runtime refused a launch."""
+
+
+@cache
+def library() -> ctypes.CDLL:
+    if not LIBRARY.exists():
+        raise RuntimeError(
+            f"{LIBRARY.name} is not built; run `python -m vflash_amd.build` (hipcc, gfx950)"
+        )
+    lib = ctypes.CDLL(str(LIBRARY))
+    for name, (args, restype) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = restype
+    if lib.vflash_abi_version() != 1:
+        raise RuntimeError("libvflash_amd.so has an unexpected ABI version")
+    return lib
+
+
+def call(name: str, *args) -> None:
+    """Invoke an entry point; map a negative status to an exception."""
+    status = getattr(library(), name)(*args)
+    if status == VFLASH_OK:
+        return
+    text = library().vflash_status_string(status).decode()
+    if status == VFLASH_EINVAL:
+        raise ValueError(f"{name}: {text}")
+    raise KernelError(f"{name}: {text}")
+
+
+@cache
+def _arch(index: int) -> str:
+    return torch.cuda.get_device_properties(index).gcnArchName
+
+
+def is_gfx950(device: torch.device) -> bool:
+    if device.type != "cuda" or not torch.cuda.is_available():
+        return False
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return _arch(index).split(":")[0] == "gfx950"
+
+
+def stream_of(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def ptr(tensor: torch.Tensor | None) -> ctypes.c_void_p | None:
+    return None if tensor is None else ctypes.c_void_p(tensor.data_ptr())
+
+
+def set_gemm_tile(tile: int, group_m: int = 0) -> int:
+    """Force a GEMM tile configuration (0 = automatic); returns the previous one."""
+    return library().vflash_set_gemm_tile(tile, group_m)

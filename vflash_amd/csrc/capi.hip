@@ -1,0 +1,224 @@
+// extern "C" entry points declared in include/vflash_amd.h.
+//
+// Each entry validates its arguments against the declared contract before any
+// launch (no work is enqueued on a negative status), builds the kernel
+// parameter block and enqueues on the caller's stream.  Nothing here
+// allocates, synchronizes or retains a pointer.
+#include <hip/hip_runtime.h>
+
+#include "../../include/vflash_amd.h"
+#include "common.h"
+#include "gemm_params.h"
+
+namespace vfa {
+hipError_t launch_quant_rows(const uint16_t*, int64_t, int64_t, int64_t, uint8_t*, float*,
+                             int64_t, hipStream_t);
+hipError_t launch_requant_rows(const uint16_t*, int64_t, int64_t, int64_t, const float*, int,
+                               uint8_t*, float*, int64_t, hipStream_t);
+hipError_t launch_fp8_gemm(const GemmParams&, int, hipStream_t);
+hipError_t launch_lora_down(const uint16_t*, int64_t, int64_t, int64_t, const uint16_t*, int,
+                            uint16_t*, hipStream_t);
+hipError_t launch_nvfp4(const uint8_t*, const float*, int64_t, const uint8_t*, const uint8_t*,
+                        const float*, int64_t, int64_t, int64_t, const uint16_t*, uint16_t*, int64_t, int,
+                        int, hipStream_t);
+}  // namespace vfa
+
+namespace {
+
+int g_tile = 0;     // tuning override (0 = automatic)
+int g_group_m = 8;  // tile-order group height
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+int status(hipError_t e) { return e == hipSuccess ? VFLASH_OK : VFLASH_ELAUNCH; }
+
+// Shared contract of every E4M3 GEMM entry point.
+bool gemm_args_ok(const void* a, const float* sa, int64_t lda, const void* w, const float* sw,
+                  int64_t ldw, int64_t m, int64_t n, int64_t k, const void* bias) {
+  if (!a || !sa || !w || !sw) return false;
+  if (m < 1 || n < 1 || k < 16) return false;
+  if (k % 16 || n % 16 || lda < k || ldw < k || lda % 16 || ldw % 16) return false;
+  if (!aligned(a, 16) || !aligned(w, 16) || !aligned(sa, 4) || !aligned(sw, 4)) return false;
+  if (bias && !aligned(bias, 8)) return false;
+  // Per-tile buffer ranges (at most 256 rows) must stay below 2^31 bytes.
+  if (256 * lda >= (int64_t(1) << 31) || 256 * ldw >= (int64_t(1) << 31)) return false;
+  if (m >= (int64_t(1) << 31) / 256 * 256 || n >= (int64_t(1) << 31)) return false;
+  return true;
+}
+
+vfa::GemmParams base_params(const void* a, const float* sa, int64_t lda, const void* w,
+                            const float* sw, int64_t ldw, int64_t m, int64_t n, int64_t k,
+                            const void* bias, void* out, int64_t ldo) {
+  vfa::GemmParams p{};
+  p.a = static_cast<const uint8_t*>(a);
+  p.sa = sa;
+  p.w = static_cast<const uint8_t*>(w);
+  p.sw = sw;
+  p.lda = lda;
+  p.ldw = ldw;
+  p.m = m;
+  p.n = n;
+  p.k = k;
+  p.bias = static_cast<const uint16_t*>(bias);
+  p.out = static_cast<uint16_t*>(out);
+  p.ldo = ldo;
+  p.lora_scale = 1.0f;
+  p.lora_strength = 1.0f;
+  p.group_m = g_group_m;
+  p.tile = g_tile;
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vflash_abi_version(void) { return 1; }
+
+const char* vflash_status_string(int s) {
+  switch (s) {
+    case VFLASH_OK: return "ok";
+    case VFLASH_EINVAL: return "argument outside the declared contract";
+    case VFLASH_ELAUNCH: return "HIP launch failed";
+    default: return "unknown status";
+  }
+}
+
+int vflash_set_gemm_tile(int tile, int group_m) {
+  const int prev = g_tile;
+  if (tile >= 0 && tile <= 5) g_tile = tile;
+  g_group_m = group_m > 0 ? group_m : 8;
+  return prev;
+}
+
+int vflash_quantize_rows_e4m3(const void* x, int64_t m, int64_t k, int64_t ldx, void* codes,
+                              float* scales, int64_t m_pad, void* stream) {
+  if (!x || !codes || !scales || m < 1 || k < 1 || ldx < k || m_pad < m) return VFLASH_EINVAL;
+  if (!aligned(x, 2) || !aligned(scales, 4) || m_pad >= (int64_t(1) << 33)) return VFLASH_EINVAL;
+  return status(vfa::launch_quant_rows(static_cast<const uint16_t*>(x), m, k, ldx,
+                                       static_cast<uint8_t*>(codes), scales, m_pad,
+                                       static_cast<hipStream_t>(stream)));
+}
+
+int vflash_fp8_linear(const void* a, const float* sa, int64_t lda, const void* w,
+                      const float* sw, int64_t ldw, int64_t m, int64_t n, int64_t k,
+                      const void* bias, void* out, int64_t ldo, void* stream) {
+  if (!gemm_args_ok(a, sa, lda, w, sw, ldw, m, n, k, bias)) return VFLASH_EINVAL;
+  if (!out || ldo < n || ldo % 4 || !aligned(out, 8)) return VFLASH_EINVAL;
+  vfa::GemmParams p = base_params(a, sa, lda, w, sw, ldw, m, n, k, bias, out, ldo);
+  return status(vfa::launch_fp8_gemm(p, vfa::EPI_BIAS, static_cast<hipStream_t>(stream)));
+}
+
+int vflash_fp8_linear_planes(const void* a, const float* sa, int64_t lda, const void* w,
+                             const float* sw, int64_t ldw, int64_t m, int64_t n, int64_t k,
+                             const void* bias, void* out, int64_t ldo, int64_t plane_cols,
+                             int64_t plane_stride, void* stream) {
+  if (!gemm_args_ok(a, sa, lda, w, sw, ldw, m, n, k, bias)) return VFLASH_EINVAL;
+  if (plane_cols < 16 || plane_cols % 16 || n % plane_cols) return VFLASH_EINVAL;
+  if (!out || ldo < plane_cols || ldo % 4 || plane_stride % 4 || !aligned(out, 8))
+    return VFLASH_EINVAL;
+  if (plane_stride < (m - 1) * ldo + plane_cols) return VFLASH_EINVAL;  // planes may not overlap
+  vfa::GemmParams p = base_params(a, sa, lda, w, sw, ldw, m, n, k, bias, out, ldo);
+  p.plane_cols = plane_cols;
+  p.plane_stride = plane_stride;
+  return status(vfa::launch_fp8_gemm(p, vfa::EPI_BIAS, static_cast<hipStream_t>(stream)));
+}
+
+int64_t vflash_row_parts(int64_t n) { return n > 0 ? (n + 63) / 64 : 0; }
+
+int vflash_fp8_linear_gelu(const void* a, const float* sa, int64_t lda, const void* w,
+                           const float* sw, int64_t ldw, int64_t m, int64_t n, int64_t k,
+                           const void* bias, void* g, int64_t ldg, float* amax_part,
+                           void* stream) {
+  if (!gemm_args_ok(a, sa, lda, w, sw, ldw, m, n, k, bias)) return VFLASH_EINVAL;
+  if (!g || !amax_part || ldg < n || ldg % 4 || !aligned(g, 8) || !aligned(amax_part, 4))
+    return VFLASH_EINVAL;
+  vfa::GemmParams p = base_params(a, sa, lda, w, sw, ldw, m, n, k, bias, g, ldg);
+  p.amax_part = amax_part;
+  return status(vfa::launch_fp8_gemm(p, vfa::EPI_GELU, static_cast<hipStream_t>(stream)));
+}
+
+int vflash_requant_rows_e4m3(const void* g, int64_t m, int64_t k, int64_t ldg,
+                             const float* amax_part, int64_t parts, void* codes, float* scales,
+                             int64_t m_pad, void* stream) {
+  if (!g || !amax_part || !codes || !scales || m < 1 || k < 8 || m_pad < m) return VFLASH_EINVAL;
+  if (k % 8 || ldg < k || ldg % 8 || !aligned(g, 16) || !aligned(codes, 8)) return VFLASH_EINVAL;
+  if (parts < 1 || parts > (int64_t(1) << 30) || !aligned(scales, 4)) return VFLASH_EINVAL;
+  return status(vfa::launch_requant_rows(static_cast<const uint16_t*>(g), m, k, ldg, amax_part,
+                                         (int)parts, static_cast<uint8_t*>(codes), scales, m_pad,
+                                         static_cast<hipStream_t>(stream)));
+}
+
+int vflash_fp8_linear_gate_residual(const void* a, const float* sa, int64_t lda, const void* w,
+                                    const float* sw, int64_t ldw, int64_t m, int64_t n,
+                                    int64_t k, const void* bias, const void* gate,
+                                    int64_t gate_ts, int64_t gate_hs, const void* residual,
+                                    int64_t ldr, void* out, int64_t ldo, void* stream) {
+  if (!gemm_args_ok(a, sa, lda, w, sw, ldw, m, n, k, bias)) return VFLASH_EINVAL;
+  if (!gate || !residual || !out || ldo < n || ldr < n || ldo % 4 || !aligned(out, 8))
+    return VFLASH_EINVAL;
+  if (gate_ts < 0 || gate_hs < 0 || !aligned(gate, 2) || !aligned(residual, 2))
+    return VFLASH_EINVAL;
+  if (out == residual && ldo != ldr) return VFLASH_EINVAL;
+  vfa::GemmParams p = base_params(a, sa, lda, w, sw, ldw, m, n, k, bias, out, ldo);
+  p.gate = static_cast<const uint16_t*>(gate);
+  p.gate_ts = gate_ts;
+  p.gate_hs = gate_hs;
+  p.residual = static_cast<const uint16_t*>(residual);
+  p.ldr = ldr;
+  return status(vfa::launch_fp8_gemm(p, vfa::EPI_GATE, static_cast<hipStream_t>(stream)));
+}
+
+int vflash_lora_down(const void* x, int64_t m, int64_t k, int64_t ldx, const void* lora_a,
+                     int64_t rank, void* t, void* stream) {
+  if (!x || !lora_a || !t || m < 1 || k < 16 || k % 16 || ldx < k || ldx % 8) return VFLASH_EINVAL;
+  if (rank < 16 || rank > 128 || rank % 16) return VFLASH_EINVAL;
+  if (!aligned(x, 16) || !aligned(lora_a, 16) || !aligned(t, 8)) return VFLASH_EINVAL;
+  return status(vfa::launch_lora_down(static_cast<const uint16_t*>(x), m, k, ldx,
+                                      static_cast<const uint16_t*>(lora_a), (int)rank,
+                                      static_cast<uint16_t*>(t),
+                                      static_cast<hipStream_t>(stream)));
+}
+
+int vflash_fp8_linear_lora(const void* a, const float* sa, int64_t lda, const void* w,
+                           const float* sw, int64_t ldw, int64_t m, int64_t n, int64_t k,
+                           const void* bias, const void* t, int64_t ldt, const void* lora_b,
+                           int64_t ldb, int64_t rank, float scale, float strength, void* out,
+                           int64_t ldo, void* stream) {
+  if (!gemm_args_ok(a, sa, lda, w, sw, ldw, m, n, k, bias)) return VFLASH_EINVAL;
+  if (!t || !lora_b || !out || ldo < n || ldo % 4 || !aligned(out, 8)) return VFLASH_EINVAL;
+  if (rank < 16 || rank > 128 || rank % 16 || ldt < rank || ldb < rank || ldt % 8 || ldb % 8)
+    return VFLASH_EINVAL;
+  if (!aligned(t, 16) || !aligned(lora_b, 16)) return VFLASH_EINVAL;
+  vfa::GemmParams p = base_params(a, sa, lda, w, sw, ldw, m, n, k, bias, out, ldo);
+  p.lora_t = static_cast<const uint16_t*>(t);
+  p.ldt = ldt;
+  p.lora_b = static_cast<const uint16_t*>(lora_b);
+  p.ldb = ldb;
+  p.rank = (int)rank;
+  p.lora_scale = scale;
+  p.lora_strength = strength;
+  return status(vfa::launch_fp8_gemm(p, vfa::EPI_LORA, static_cast<hipStream_t>(stream)));
+}
+
+int vflash_nvfp4_linear(const void* a, const float* sa, int64_t lda, const void* w_packed,
+                        const void* w_scales, const float* alpha, int64_t m, int64_t n, int64_t k,
+                        const void* bias, void* out, int64_t ldo, void* stream) {
+  if (!a || !sa || !w_packed || !w_scales || !alpha || !out || m < 1 || n < 128 || k < 64)
+    return VFLASH_EINVAL;
+  if (n % 128 || k % 64 || lda < k || lda % 16 || ldo < n || ldo % 4) return VFLASH_EINVAL;
+  if (!aligned(a, 16) || !aligned(w_packed, 16) || !aligned(w_scales, 2) || !aligned(out, 8))
+    return VFLASH_EINVAL;
+  if (bias && !aligned(bias, 2)) return VFLASH_EINVAL;
+  if (!aligned(alpha, 4)) return VFLASH_EINVAL;
+  if (256 * lda >= (int64_t(1) << 31)) return VFLASH_EINVAL;
+  const int tile = (g_tile >= 1 && g_tile <= 3) ? g_tile : 0;
+  return status(vfa::launch_nvfp4(static_cast<const uint8_t*>(a), sa, lda,
+                                  static_cast<const uint8_t*>(w_packed),
+                                  static_cast<const uint8_t*>(w_scales), alpha, m, n, k,
+                                  static_cast<const uint16_t*>(bias),
+                                  static_cast<uint16_t*>(out), ldo, tile, g_group_m,
+                                  static_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

@@ -1,0 +1,113 @@
+// Device helpers shared by the gfx950 kernels of the quantized-linear path.
+//
+// Number formats follow the OCP 8-bit floating point specification (E4M3 with
+// no infinities, max 448, NaN = S.1111.111) and the OCP MX specification for
+// E2M1 (values 0, 0.5, 1, 1.5, 2, 3, 4, 6).  bfloat16 is the upper half of an
+// IEEE binary32.  All conversions here are written from those definitions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vfa {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+
+// The binary32 value of FLT_MIN (2^-126), the floor of every row scale.
+#define VFA_FLT_MIN 1.1754943508222875e-38f
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+
+// binary32 -> bfloat16, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// Round a binary32 to the nearest bfloat16 and widen it back.
+__device__ __forceinline__ float round_bf16(float f) {
+  return bf16_to_f32(f32_to_bf16(f));
+}
+
+// binary32 -> E4M3 (OCP "fn" variant) with round to nearest even.  The caller
+// has already clamped |f| <= 448, so the result never overflows; NaN maps to
+// the NaN code with the input's sign.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
+  uint32_t u = __float_as_uint(f);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7fu;
+  uint32_t code;
+  if (a < 0x3c800000u) {
+    // Below 2^-6 the format is uniform with step 2^-9: scale by 2^9 (exact)
+    // and round to an integer 0..8; 8 is the encoding of 2^-6 itself.
+    code = (uint32_t)__builtin_rintf(__uint_as_float(a) * 512.0f);
+  } else {
+    // Normal range: re-bias the exponent (127 -> 7) and round the 23-bit
+    // mantissa to 3 bits; a carry moves into the exponent field as it should.
+    uint32_t t = a - (120u << 23);
+    t += 0x7ffffu + ((t >> 20) & 1u);
+    code = t >> 20;
+  }
+  return sign | code;
+}
+
+__device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
+  uint32_t s = (c & 0x80u) << 24;
+  uint32_t e = (c >> 3) & 0xfu;
+  uint32_t m = c & 7u;
+  float v;
+  if ((c & 0x7fu) == 0x7fu) return __uint_as_float(s | 0x7fc00000u);
+  if (e == 0) v = (float)m * (1.0f / 512.0f);
+  else v = __uint_as_float(((e + 120u) << 23) | (m << 20));
+  return __uint_as_float(__float_as_uint(v) | s);
+}
+
+// Raw buffer resources: loads outside [0, num_records) return zero and stores
+// there are dropped, which gives free bounds checks at tile edges.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+// An offset that is always past num_records (num_records < 2^31 by construction).
+#define VFA_OOB 0x80000000u
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// tanh-approximated GELU in binary32: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))).
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float beta = 0.7978845608028654f;  // sqrt(2/pi)
+  const float kappa = 0.044715f;
+  float inner = beta * (x + kappa * x * x * x);
+  return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+// E2M1 (OCP MX): bit 3 sign, bits 2..1 exponent (bias 1), bit 0 mantissa.
+// Codes 0..7 are 0, .5, 1, 1.5, 2, 3, 4, 6.  Built as binary32 bits directly.
+__device__ __forceinline__ float e2m1_to_f32(uint32_t c) {
+  uint32_t e = (c >> 1) & 3u, m = c & 1u;
+  uint32_t bits = e ? (((e + 126u) << 23) | (m << 22)) : (m ? 0x3f000000u : 0u);
+  return __uint_as_float(bits | ((c & 8u) << 28));
+}
+
+}  // namespace vfa

@@ -1,0 +1,35 @@
+// Kernel-side parameter block of the E4M3 GEMM family (not part of the C-ABI).
+#pragma once
+#include <stdint.h>
+
+namespace vfa {
+
+enum { EPI_BIAS = 0, EPI_GELU = 1, EPI_GATE = 2, EPI_LORA = 3 };
+
+struct GemmParams {
+  const uint8_t* a;  // activation codes [m, k], row stride lda bytes
+  const float* sa;   // per-row activation scales [m]
+  const uint8_t* w;  // weight codes [n, k], row stride ldw bytes
+  const float* sw;   // per-output-channel weight scales [n]
+  int64_t lda, ldw, m, n, k;
+  const uint16_t* bias;  // bf16 [n] or null
+  uint16_t* out;         // bf16, row stride ldo elements
+  int64_t ldo;
+  int64_t plane_cols;    // > 0: column n goes to plane n / plane_cols
+  int64_t plane_stride;  // elements between planes
+  float* amax_part;      // EPI_GELU: [m, ceil(n / 64)] per-row maxima of |out|
+  const uint16_t* gate;  // EPI_GATE: gate[m * gate_ts + n * gate_hs]
+  int64_t gate_ts, gate_hs;
+  const uint16_t* residual;  // EPI_GATE: residual[m * ldr + n]
+  int64_t ldr;
+  const uint16_t* lora_t;  // EPI_LORA: t[m * ldt + r], bf16
+  int64_t ldt;
+  const uint16_t* lora_b;  // EPI_LORA: B[n * ldb + r], bf16
+  int64_t ldb;
+  int rank;
+  float lora_scale, lora_strength;
+  int group_m;  // tile-order group height
+  int tile;     // tile configuration (0 = automatic)
+};
+
+}  // namespace vfa

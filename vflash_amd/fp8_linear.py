@@ -1,0 +1,155 @@
+"""Row-scaled E4M3 linear execution on MI355X (drop-in for the reference module).
+
+Mirrors ``RowFP8Execution`` / ``RowFP8Linear`` of the reference
+(src/vflash/native/h3_fp8_linear.py:34-149): same constructor arguments,
+attributes, counters, observer cadence, ``measure`` scope names, validation
+order and error conditions.  The W8A8 mode runs the HIP kernels of this
+package on gfx950 and never falls back to another arithmetic:
+
+* activation quantization: ``vflash_quantize_rows_e4m3`` (the fused kernel;
+  ``activation_quantizer="triton"`` is accepted as the name of the reference's
+  fused quantizer and selects the same HIP kernel), or the portable torch
+  expression for ``"torch"``;
+* GEMM + scales + bias: ``vflash_fp8_linear`` with binary32 accumulation and
+  the reference's two bf16 roundings (``_scaled_mm`` output, then ``+ bias``).
+
+``fast_accum`` is validated and recorded like the reference's; MFMA
+accumulation is always binary32, so it does not change the arithmetic.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Callable
+from contextlib import AbstractContextManager, nullcontext
+from typing import Any
+
+import torch
+
+from vflash_amd import _lib, kernels
+
+
+def _quantize_activation_torch(matrix):
+    """Portable torch expression of the row quantizer, with 16-row GEMM padding.
+
+    Same arithmetic as h3_fp8_linear.py:18-31 (and the HIP kernel): fp32 row
+    maximum, ``scale = max(amax / 448, FLT_MIN)`` (1 for a zero row), codes
+    ``e4m3(clamp(x / scale, -448, 448))``.
+    """
+    rows = matrix.shape[0]
+    if rows % 16:
+        matrix = torch.nn.functional.pad(matrix, (0, 0, 0, 16 - rows % 16))
+    floats = matrix.float()
+    maxima = floats.abs().amax(dim=1, keepdim=True)
+    act_scale = torch.where(
+        maxima > 0,
+        (maxima / 448.0).clamp_min(torch.finfo(torch.float32).tiny),
+        torch.ones_like(maxima),
+    )
+    codes = (floats / act_scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return codes, act_scale
+
+
+def w8a8_supported(value: torch.Tensor) -> bool:
+    return value.dtype == torch.bfloat16 and _lib.is_gfx950(value.device)
+
+
+class RowFP8Execution:
+    """Own the precision choice and counters without changing process globals.
+
+    ``weight-only`` restores approximate weights for an ordinary GEMM.  ``w8a8``
+    uses BF16 input, E4M3 activations/weights and fp32 per-row scales on a
+    gfx950 device.  ``measure`` may supply asynchronous profiling scopes; this
+    class inserts no synchronization, environment changes or device selection.
+    """
+
+    def __init__(
+        self,
+        mode: str = "weight-only",
+        *,
+        activation_quantizer: str = "torch",
+        fast_accum: bool = False,
+        measure: Callable[[str], AbstractContextManager[Any]] | None = None,
+    ) -> None:
+        if activation_quantizer not in ("torch", "triton", "hip"):
+            raise ValueError("unknown FP8 activation quantizer")
+        if type(fast_accum) is not bool:
+            raise ValueError("fast_accum must be an explicit boolean")
+        self.activation_quantizer = activation_quantizer
+        self.fast_accum = fast_accum
+        self.measure = measure if measure is not None else lambda _name: nullcontext()
+        self.observer: Callable[[], None] | None = None
+        self.calls = {"weight_only": 0, "w8a8": 0}
+        self.select(mode)
+
+    def select(self, mode: str) -> None:
+        if mode not in ("weight-only", "w8a8"):
+            raise ValueError("unknown FP8 execution mode")
+        self.mode = mode
+
+    def linear(self, value, weight, scale, bias=None):
+        if self.observer is not None and sum(self.calls.values()) % 200 == 0:
+            self.observer()
+        if (
+            weight.ndim != 2
+            or value.ndim < 1
+            or min(weight.shape) <= 0
+            or value.shape[-1] != weight.shape[1]
+            or weight.dtype != torch.float8_e4m3fn
+            or scale.dtype != torch.float32
+            or scale.shape != (weight.shape[0], 1)
+            or weight.device != value.device
+            or scale.device != value.device
+        ):
+            raise ValueError("FP8 codes/scales differ from the declared layout")
+        if bias is not None and (
+            bias.shape != (weight.shape[0],)
+            or bias.device != value.device
+            or bias.dtype != value.dtype
+        ):
+            raise ValueError("FP8 bias differs from the declared output")
+        if self.mode == "weight-only":
+            self.calls["weight_only"] += 1
+            restored = (weight.float() * scale).to(value.dtype)
+            return torch.nn.functional.linear(value, restored, bias)
+        if not w8a8_supported(value):
+            raise ValueError("W8A8 requires gfx950 (MI355X) BF16 inputs")
+        self.calls["w8a8"] += 1
+        shape = value.shape
+        matrix = value.reshape(-1, shape[-1])
+        rows = matrix.shape[0]
+        if self.activation_quantizer == "torch":
+            codes, act_scale = _quantize_activation_torch(matrix)
+        else:
+            with self.measure("linear.activation_quantize"):
+                codes, act_scale = kernels.quantize_rows(matrix)
+        with self.measure("linear.fp8_gemm"):
+            output = kernels.fp8_gemm(codes, act_scale, weight, scale, rows, bias)
+        return output.reshape(*shape[:-1], weight.shape[0])
+
+
+class RowFP8Linear(torch.nn.Module):
+    """Meta-initialized Linear replacement; assign trusted codes and row_scale.
+
+    The original bias is preserved.  A loader must assign all meta tensors
+    before execution, and keep the intended host/device placement.
+    """
+
+    def __init__(self, original: torch.nn.Linear, execution: RowFP8Execution):
+        super().__init__()
+        self.in_features = original.in_features
+        self.out_features = original.out_features
+        self.weight = torch.nn.Parameter(
+            torch.empty(
+                (self.out_features, self.in_features), device="meta", dtype=torch.float8_e4m3fn
+            ),
+            requires_grad=False,
+        )
+        self.register_buffer(
+            "row_scale",
+            torch.empty((self.out_features, 1), device="meta", dtype=torch.float32),
+        )
+        self.bias = original.bias
+        self.execution = execution
+
+    def forward(self, value):
+        return self.execution.linear(value, self.weight, self.row_scale, self.bias)

@@ -1,0 +1,226 @@
+"""Fused W8A8 compositions: merged QKV, the GELU-tanh FFN, and the LoRA linear.
+
+Each runs on the HIP kernels of this package and keeps the rounding boundaries
+of the reference's unfused sequence:
+
+* merged QKV (src/vflash/adapters/h3_reference_execution.py:141-192): one
+  linear over ``cat(Wq, Wk, Wv)`` and ``cat(scales)``; returns the three column
+  chunks, either as views of one ``[.., 3*inner]`` output (the reference's
+  ``.chunk(3, -1)``) or as three contiguous planes (the copy done by
+  src/vflash/native/h3_tiled_block.py:45-60), written directly by the epilogue;
+* FFN: up-projection + bias + GELU-tanh in the GEMM epilogue, which also emits
+  per-row |g| maxima; per-token E4M3 requantization of ``g`` (the down
+  projection's own activation quantization); down-projection + bias + adaLN
+  gate + residual in the epilogue (h3_fused_ops.py:124-170 rounding);
+* LoRA (src/vflash/adapters/h3_reference_lora.py:75-90): ``t = bf16(x A^T)``,
+  then the base linear with ``bf16(t B^T)`` merged in its epilogue.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from vflash_amd import kernels
+from vflash_amd.fp8_linear import RowFP8Execution, _quantize_activation_torch, w8a8_supported
+
+
+def _quantize(execution: RowFP8Execution, matrix):
+    if execution.activation_quantizer == "torch":
+        return _quantize_activation_torch(matrix)
+    with execution.measure("linear.activation_quantize"):
+        return kernels.quantize_rows(matrix)
+
+
+def _check_w8a8(execution: RowFP8Execution, value, weight, scale, bias=None):
+    if execution.mode != "w8a8":
+        raise ValueError("fused FP8 compositions require a w8a8 execution")
+    if (
+        weight.ndim != 2
+        or value.ndim < 1
+        or value.shape[-1] != weight.shape[1]
+        or weight.dtype != torch.float8_e4m3fn
+        or scale.dtype != torch.float32
+        or scale.shape != (weight.shape[0], 1)
+        or weight.device != value.device
+        or scale.device != value.device
+    ):
+        raise ValueError("FP8 codes/scales differ from the declared layout")
+    if bias is not None and (
+        bias.shape != (weight.shape[0],) or bias.device != value.device or bias.dtype != value.dtype
+    ):
+        raise ValueError("FP8 bias differs from the declared output")
+    if not w8a8_supported(value):
+        raise ValueError("W8A8 requires gfx950 (MI355X) BF16 inputs")
+
+
+def merge_qkv(weights, scales):
+    """Concatenate per-projection codes [inner, hidden] and row scales [inner, 1]."""
+    if len(weights) != 3 or len(scales) != 3:
+        raise ValueError("merged QKV needs exactly three projections")
+    if any(w.shape != weights[0].shape or w.dtype != torch.float8_e4m3fn for w in weights):
+        raise ValueError("QKV fusion requires matching cached row-FP8 projections")
+    return torch.cat([w.detach() for w in weights]), torch.cat(list(scales))
+
+
+def qkv_linear(execution: RowFP8Execution, value, weight, scale, bias=None, *, planes=False):
+    """One W8A8 linear over the merged [3*inner, hidden] matrix.
+
+    ``planes=False`` returns ``.chunk(3, -1)`` views of one output, exactly as
+    the reference; ``planes=True`` returns three contiguous ``[.., inner]``
+    tensors (views into one [3, rows, inner] buffer) written by the epilogue.
+    """
+    _check_w8a8(execution, value, weight, scale, bias)
+    if weight.shape[0] % 3:
+        raise ValueError("a merged QKV matrix has 3 * inner rows")
+    if execution.observer is not None and sum(execution.calls.values()) % 200 == 0:
+        execution.observer()
+    execution.calls["w8a8"] += 1
+    shape = value.shape
+    matrix = value.reshape(-1, shape[-1])
+    rows = matrix.shape[0]
+    codes, act_scale = _quantize(execution, matrix)
+    inner = weight.shape[0] // 3
+    with execution.measure("linear.fp8_gemm"):
+        if planes:
+            out = kernels.fp8_gemm_planes(codes, act_scale, weight, scale, rows, 3, bias)
+            return tuple(out[i].view(*shape[:-1], inner) for i in range(3))
+        out = kernels.fp8_gemm(codes, act_scale, weight, scale, rows, bias)
+    return out.reshape(*shape[:-1], 3 * inner).chunk(3, dim=-1)
+
+
+class FusedQKV(torch.nn.Module):
+    """Merged Q/K/V projection built from three row-FP8 projections without bias.
+
+    Mirrors the construction checks of h3_reference_execution.py:141-160: the
+    three parts must share shape, dtype and execution, and carry no bias.
+    """
+
+    def __init__(self, to_q, to_k, to_v, *, planes=False):
+        super().__init__()
+        parts = [to_q, to_k, to_v]
+        if not all(
+            hasattr(p, "execution")
+            and hasattr(p, "row_scale")
+            and p.bias is None
+            and p.weight.shape == parts[0].weight.shape
+            and p.execution is parts[0].execution
+            for p in parts
+        ):
+            raise ValueError("QKV fusion requires matching cached row-FP8 projections")
+        weight, scale = merge_qkv([p.weight for p in parts], [p.row_scale for p in parts])
+        self.weight = torch.nn.Parameter(weight, requires_grad=False)
+        self.register_buffer("row_scale", scale)
+        self.execution = parts[0].execution
+        self.planes = planes
+
+    def forward(self, value):
+        return qkv_linear(self.execution, value, self.weight, self.row_scale, planes=self.planes)
+
+
+def fp8_ffn(
+    execution: RowFP8Execution,
+    value,
+    up_weight,
+    up_scale,
+    up_bias,
+    down_weight,
+    down_scale,
+    down_bias,
+    gate,
+    residual,
+):
+    """residual + gate * down(requant(gelu_tanh(up(value)))) with reference rounding.
+
+    ``value`` and ``residual`` are ``[.., hidden]``; ``gate`` is ``[hidden]``
+    (broadcast over tokens) or ``[tokens, hidden]`` with any strides.
+    """
+    _check_w8a8(execution, value, up_weight, up_scale, up_bias)
+    hidden = up_weight.shape[1]
+    if down_weight.shape[1] != up_weight.shape[0] or down_weight.shape[0] != hidden:
+        raise ValueError("FFN up/down projections do not chain")
+    shape = value.shape
+    matrix = value.reshape(-1, hidden)
+    rows = matrix.shape[0]
+    res = residual.reshape(-1, down_weight.shape[0])
+    if res.shape[0] != rows:
+        raise ValueError("residual rows differ from the FFN input rows")
+    if execution.observer is not None and sum(execution.calls.values()) % 200 == 0:
+        execution.observer()
+    execution.calls["w8a8"] += 2
+    codes, act_scale = _quantize(execution, matrix)
+    with execution.measure("linear.fp8_gemm"):
+        g, amax = kernels.fp8_gemm_gelu(codes, act_scale, up_weight, up_scale, rows, up_bias)
+    with execution.measure("linear.activation_quantize"):
+        h_codes, h_scale = kernels.requant_rows(g, amax)
+    with execution.measure("linear.fp8_gemm"):
+        out = kernels.fp8_gemm_gate_residual(
+            h_codes, h_scale, down_weight, down_scale, rows, gate, res, down_bias
+        )
+    return out.reshape(shape)
+
+
+class FP8FeedForward(torch.nn.Module):
+    """FFN block of two row-FP8 projections with a GELU-tanh activation."""
+
+    def __init__(self, up, down):
+        super().__init__()
+        if up.execution is not down.execution:
+            raise ValueError("FFN projections must share one execution")
+        self.up, self.down, self.execution = up, down, up.execution
+
+    def forward(self, value, gate, residual):
+        return fp8_ffn(
+            self.execution,
+            value,
+            self.up.weight,
+            self.up.row_scale,
+            self.up.bias,
+            self.down.weight,
+            self.down.row_scale,
+            self.down.bias,
+            gate,
+            residual,
+        )
+
+
+def fp8_linear_lora(
+    execution: RowFP8Execution,
+    value,
+    weight,
+    scale,
+    bias,
+    lora_a,
+    lora_b,
+    *,
+    scaling: float = 1.0,
+    strength: float = 1.0,
+):
+    """W8A8 linear plus an activation-space LoRA delta merged in the epilogue.
+
+    Same result as the reference hook applied to ``execution.linear``:
+    ``result + bf16(bf16(bf16(x A^T) B^T) [* scaling] [* strength])``;
+    strength 0 skips the adapter (h3_reference_lora.py:75-78).
+    """
+    _check_w8a8(execution, value, weight, scale, bias)
+    if strength == 0.0:
+        return execution.linear(value, weight, scale, bias)
+    if lora_a.ndim != 2 or lora_b.ndim != 2 or lora_a.shape[1] != weight.shape[1]:
+        raise ValueError("Adapter projection does not match the target model")
+    if lora_b.shape != (weight.shape[0], lora_a.shape[0]):
+        raise ValueError("Adapter projection does not match the target model")
+    if execution.observer is not None and sum(execution.calls.values()) % 200 == 0:
+        execution.observer()
+    execution.calls["w8a8"] += 1
+    shape = value.shape
+    matrix = value.reshape(-1, shape[-1])
+    rows = matrix.shape[0]
+    if matrix.stride(1) != 1 or matrix.stride(0) % 8:
+        matrix = matrix.contiguous()
+    codes, act_scale = _quantize(execution, matrix)
+    t = kernels.lora_down(matrix, lora_a)
+    with execution.measure("linear.fp8_gemm"):
+        out = kernels.fp8_gemm_lora(
+            codes, act_scale, weight, scale, rows, t, lora_b, scale=scaling, strength=strength,
+            bias=bias,
+        )
+    return out.reshape(*shape[:-1], weight.shape[0])

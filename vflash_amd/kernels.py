@@ -1,0 +1,221 @@
+"""Tensor-level wrappers of the HIP kernels (one call = one C-ABI entry).
+
+Each wrapper checks dtypes, devices and layouts, allocates its outputs with
+``torch.empty`` on the input's device and enqueues on the current stream.
+No wrapper synchronizes.  Unsupported devices raise ``ValueError``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from vflash_amd import _lib
+from vflash_amd._lib import call, ptr, stream_of
+
+E4M3 = torch.float8_e4m3fn
+
+
+def require_device(*tensors: torch.Tensor) -> torch.device:
+    device = tensors[0].device
+    if not _lib.is_gfx950(device):
+        raise ValueError("the HIP quantized-linear kernels require a gfx950 (MI355X) device")
+    for t in tensors:
+        if t is not None and t.device != device:
+            raise ValueError("all operands must share one device")
+    return device
+
+
+def padded_rows(rows: int) -> int:
+    return (rows + 15) // 16 * 16
+
+
+def quantize_rows(matrix: torch.Tensor, pad_to: int = 16):
+    """Per-token E4M3 codes [ceil16(M), K] and fp32 scales [ceil16(M), 1]."""
+    if matrix.dtype != torch.bfloat16 or matrix.ndim != 2 or matrix.stride(1) != 1:
+        raise ValueError("row quantization requires a 2-D BF16 matrix with unit column stride")
+    device = require_device(matrix)
+    m, k = matrix.shape
+    m_pad = (m + pad_to - 1) // pad_to * pad_to
+    codes = torch.empty((m_pad, k), device=device, dtype=E4M3)
+    scales = torch.empty((m_pad, 1), device=device, dtype=torch.float32)
+    if m_pad:
+        call("vflash_quantize_rows_e4m3", ptr(matrix), m, k, matrix.stride(0), ptr(codes),
+             ptr(scales), m_pad, stream_of(device))
+    return codes, scales
+
+
+def _gemm_operands(codes, act_scale, weight, w_scale, rows, bias):
+    if codes.dtype != E4M3 or weight.dtype != E4M3 or codes.ndim != 2 or weight.ndim != 2:
+        raise ValueError("E4M3 GEMM operands must be 2-D float8_e4m3fn matrices")
+    if codes.stride(1) != 1 or weight.stride(1) != 1 or codes.shape[1] != weight.shape[1]:
+        raise ValueError("E4M3 GEMM operands must share K with unit column stride")
+    if act_scale.dtype != torch.float32 or w_scale.dtype != torch.float32:
+        raise ValueError("GEMM scales must be fp32")
+    if not act_scale.is_contiguous() or not w_scale.is_contiguous():
+        raise ValueError("GEMM scales must be contiguous")
+    if act_scale.numel() < rows or w_scale.numel() != weight.shape[0] or codes.shape[0] < rows:
+        raise ValueError("GEMM scales do not cover the operands")
+    if bias is not None and (
+        bias.dtype != torch.bfloat16 or bias.shape != (weight.shape[0],) or not bias.is_contiguous()
+    ):
+        raise ValueError("GEMM bias must be a contiguous BF16 vector of the output width")
+    return require_device(codes, act_scale, weight, w_scale, *( [bias] if bias is not None else []))
+
+
+def fp8_gemm(codes, act_scale, weight, w_scale, rows, bias=None, out=None):
+    """out[rows, N] = bf16(bf16(codes . weight^T * act_scale * w_scale) + bias)."""
+    device = _gemm_operands(codes, act_scale, weight, w_scale, rows, bias)
+    n, k = weight.shape
+    if out is None:
+        out = torch.empty((rows, n), device=device, dtype=torch.bfloat16)
+    if out.dtype != torch.bfloat16 or out.shape != (rows, n) or out.stride(1) != 1:
+        raise ValueError("GEMM output must be BF16 [rows, N] with unit column stride")
+    if rows:
+        call("vflash_fp8_linear", ptr(codes), ptr(act_scale), codes.stride(0), ptr(weight),
+             ptr(w_scale), weight.stride(0), rows, n, k, ptr(bias), ptr(out), out.stride(0),
+             stream_of(device))
+    return out
+
+
+def fp8_gemm_planes(codes, act_scale, weight, w_scale, rows, planes, bias=None):
+    """Merged projection written as ``planes`` contiguous [rows, N / planes] matrices.
+
+    Returns a tensor of shape [planes, rows, N / planes].
+    """
+    device = _gemm_operands(codes, act_scale, weight, w_scale, rows, bias)
+    n, k = weight.shape
+    if planes < 1 or n % planes:
+        raise ValueError("the merged width must split evenly into planes")
+    cols = n // planes
+    out = torch.empty((planes, rows, cols), device=device, dtype=torch.bfloat16)
+    if rows:
+        call("vflash_fp8_linear_planes", ptr(codes), ptr(act_scale), codes.stride(0), ptr(weight),
+             ptr(w_scale), weight.stride(0), rows, n, k, ptr(bias), ptr(out), cols, cols,
+             rows * cols, stream_of(device))
+    return out
+
+
+def row_parts(n: int) -> int:
+    return int(_lib.library().vflash_row_parts(n))
+
+
+def fp8_gemm_gelu(codes, act_scale, weight, w_scale, rows, bias=None):
+    """g = bf16(gelu_tanh(linear)), plus per-row |g| maxima per 64-column group."""
+    device = _gemm_operands(codes, act_scale, weight, w_scale, rows, bias)
+    n, k = weight.shape
+    g = torch.empty((rows, n), device=device, dtype=torch.bfloat16)
+    parts = row_parts(n)
+    amax = torch.empty((rows, parts), device=device, dtype=torch.float32)
+    if rows:
+        call("vflash_fp8_linear_gelu", ptr(codes), ptr(act_scale), codes.stride(0), ptr(weight),
+             ptr(w_scale), weight.stride(0), rows, n, k, ptr(bias), ptr(g), g.stride(0),
+             ptr(amax), stream_of(device))
+    return g, amax
+
+
+def requant_rows(g, amax_part, pad_to: int = 16):
+    """E4M3 codes/scales of ``g`` using its epilogue row maxima."""
+    if g.dtype != torch.bfloat16 or g.ndim != 2 or g.stride(1) != 1:
+        raise ValueError("requantization requires a 2-D BF16 matrix with unit column stride")
+    if amax_part.dtype != torch.float32 or amax_part.shape[0] != g.shape[0]:
+        raise ValueError("row maxima must be fp32 [rows, parts]")
+    if not amax_part.is_contiguous():
+        raise ValueError("row maxima must be contiguous")
+    device = require_device(g, amax_part)
+    m, k = g.shape
+    m_pad = (m + pad_to - 1) // pad_to * pad_to
+    codes = torch.empty((m_pad, k), device=device, dtype=E4M3)
+    scales = torch.empty((m_pad, 1), device=device, dtype=torch.float32)
+    if m:
+        call("vflash_requant_rows_e4m3", ptr(g), m, k, g.stride(0), ptr(amax_part),
+             amax_part.shape[1], ptr(codes), ptr(scales), m_pad, stream_of(device))
+    return codes, scales
+
+
+def fp8_gemm_gate_residual(codes, act_scale, weight, w_scale, rows, gate, residual, bias=None,
+                           out=None):
+    """out = bf16(residual + bf16(gate * linear)); gate is [N] or [rows, N] (any strides)."""
+    device = _gemm_operands(codes, act_scale, weight, w_scale, rows, bias)
+    n, k = weight.shape
+    if gate.dtype != torch.bfloat16 or residual.dtype != torch.bfloat16:
+        raise ValueError("gate and residual must be BF16")
+    if gate.ndim == 1:
+        if gate.shape != (n,):
+            raise ValueError("a broadcast gate must have the output width")
+        gts, ghs = 0, gate.stride(0)
+    elif gate.ndim == 2 and gate.shape == (rows, n):
+        gts, ghs = gate.stride(0), gate.stride(1)
+    else:
+        raise ValueError("gate must be [N] or [rows, N]")
+    if residual.shape != (rows, n) or residual.stride(1) != 1:
+        raise ValueError("residual must be [rows, N] with unit column stride")
+    require_device(gate, residual)
+    if out is None:
+        out = torch.empty((rows, n), device=device, dtype=torch.bfloat16)
+    if rows:
+        call("vflash_fp8_linear_gate_residual", ptr(codes), ptr(act_scale), codes.stride(0),
+             ptr(weight), ptr(w_scale), weight.stride(0), rows, n, k, ptr(bias), ptr(gate), gts,
+             ghs, ptr(residual), residual.stride(0), ptr(out), out.stride(0), stream_of(device))
+    return out
+
+
+def lora_down(x, lora_a):
+    """t = bf16(x . lora_a^T) for a BF16 activation matrix and a BF16 [rank, K] adapter."""
+    if x.dtype != torch.bfloat16 or x.ndim != 2 or x.stride(1) != 1:
+        raise ValueError("LoRA input must be a 2-D BF16 matrix with unit column stride")
+    if lora_a.dtype != torch.bfloat16 or lora_a.ndim != 2 or not lora_a.is_contiguous():
+        raise ValueError("LoRA A must be a contiguous BF16 [rank, K] matrix")
+    device = require_device(x, lora_a)
+    m, k = x.shape
+    rank = lora_a.shape[0]
+    if lora_a.shape[1] != k:
+        raise ValueError("LoRA A does not match the input width")
+    t = torch.empty((m, rank), device=device, dtype=torch.bfloat16)
+    if m:
+        call("vflash_lora_down", ptr(x), m, k, x.stride(0), ptr(lora_a), rank, ptr(t),
+             stream_of(device))
+    return t
+
+
+def fp8_gemm_lora(codes, act_scale, weight, w_scale, rows, t, lora_b, *, scale=1.0,
+                  strength=1.0, bias=None):
+    """out = bf16(linear + delta) with delta = bf16(t . lora_b^T) [* scale] [* strength]."""
+    device = _gemm_operands(codes, act_scale, weight, w_scale, rows, bias)
+    n, k = weight.shape
+    if t.dtype != torch.bfloat16 or lora_b.dtype != torch.bfloat16:
+        raise ValueError("LoRA operands must be BF16")
+    rank = lora_b.shape[1]
+    if t.shape != (rows, rank) or lora_b.shape != (n, rank):
+        raise ValueError("LoRA operands do not match the projection")
+    if t.stride(1) != 1 or lora_b.stride(1) != 1:
+        raise ValueError("LoRA operands need unit column stride")
+    require_device(t, lora_b)
+    out = torch.empty((rows, n), device=device, dtype=torch.bfloat16)
+    if rows:
+        call("vflash_fp8_linear_lora", ptr(codes), ptr(act_scale), codes.stride(0), ptr(weight),
+             ptr(w_scale), weight.stride(0), rows, n, k, ptr(bias), ptr(t), t.stride(0),
+             ptr(lora_b), lora_b.stride(0), rank, float(scale), float(strength), ptr(out),
+             out.stride(0), stream_of(device))
+    return out
+
+
+def nvfp4_gemm(codes, act_scale, packed, block_scales, alpha, rows, bias=None):
+    """W4A8 NVFP4-weight GEMM: out[rows, N] bf16."""
+    if codes.dtype != E4M3 or codes.ndim != 2 or codes.stride(1) != 1:
+        raise ValueError("NVFP4 activation codes must be a 2-D float8_e4m3fn matrix")
+    if packed.dtype != torch.uint8 or block_scales.dtype != torch.uint8:
+        raise ValueError("NVFP4 weights and block scales must be uint8")
+    n, half_k = packed.shape
+    k = 2 * half_k
+    if codes.shape[1] != k:
+        raise ValueError("NVFP4 activation width differs from the weight")
+    if alpha.dtype != torch.float32 or alpha.numel() != 1:
+        raise ValueError("NVFP4 alpha must be an fp32 scalar tensor")
+    device = require_device(codes, act_scale, packed, block_scales, alpha,
+                            *([bias] if bias is not None else []))
+    out = torch.empty((rows, n), device=device, dtype=torch.bfloat16)
+    if rows:
+        call("vflash_nvfp4_linear", ptr(codes), ptr(act_scale), codes.stride(0), ptr(packed),
+             ptr(block_scales), ptr(alpha), rows, n, k, ptr(bias), ptr(out), out.stride(0),
+             stream_of(device))
+    return out
