@@ -167,7 +167,8 @@ int vflash_nvfp4_linear(const void* a, const float* sa, int64_t lda, const void*
 
 /*
  * Tuning hook: force a GEMM tile configuration for later calls in this process
- * (0 = automatic, 1 = 256x256, 2 = 128x128, 3 = 64x64, 4 = 128x256, 5 = 256x128)
+ * (0 = automatic, 1 = 256x256, 2 = 128x128, 3 = 64x64, 4 = 128x256, 5 = 256x128,
+ * 6 = 256x256 with 8 waves 4x2, 7 = 256x256 with 8 waves 2x4)
  * and the tile-order group height (0 = default).  Returns the previous tile value.
  */
 int vflash_set_gemm_tile(int tile, int group_m);

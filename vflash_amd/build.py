@@ -32,7 +32,7 @@ def hipcc() -> str:
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
-    "-std=c++17",
+    "-std=c++20",
     "-fPIC",
     "-Xclang",
     "-target-feature",

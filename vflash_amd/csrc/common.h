@@ -9,7 +9,18 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace vfa {
+
+// Compile-time loop: f(std::integral_constant<int, i>) for i in [0, N).  Keeps
+// every index into accumulator arrays a constant, so they stay in registers.
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  [&]<int... I>(std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+  }(std::make_integer_sequence<int, N>{});
+}
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));
@@ -78,6 +89,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            0x00020000);
 }
+
+// LDS tiles store rows of eight 16-byte chunks; chunk j of row r sits in slot
+// j ^ lds_swizzle(r).  For the rows read together by one ds_read_b128 (16
+// consecutive rows for a 64-bank LDS, 8 for a 32-bank one) the slots, taken
+// modulo the bank width, are all distinct, so fragment reads are conflict free.
+// The key depends on row bits 0..3 only: rows congruent modulo 16 share it.
+__device__ __forceinline__ int lds_swizzle(int row) { return (row ^ ((row >> 3) & 1)) & 7; }
 
 // An offset that is always past num_records (num_records < 2^31 by construction).
 #define VFA_OOB 0x80000000u

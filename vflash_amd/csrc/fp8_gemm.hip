@@ -16,13 +16,13 @@
 //              bf16(delta * scale), bf16(delta * strength) steps
 //              (adapters/h3_reference_lora.py:75-90)
 //
-// Tiling: a 256-thread workgroup (4 waves, 2x2) computes a BM x BN tile; each
-// wave owns (BM/2) x (BN/2) as 32x32 blocks of v_mfma_f32_32x32x64_f8f6f4.
+// Tiling: a workgroup of WGM x WGN waves computes a BM x BN tile; each wave
+// owns (BM/WGM) x (BN/WGN) as 32x32 blocks of v_mfma_f32_32x32x64_f8f6f4.
 // The weight fragment is MFMA operand A and the activation fragment operand B,
 // so a lane's accumulator holds 4 consecutive output columns of one row.
 // K advances 128 bytes per stage; A/W tiles are double buffered in LDS with a
-// 16-byte-chunk XOR swizzle (chunk ^ (row & 7)) so that ds_read_b128 of eight
-// consecutive rows touches eight distinct bank groups.
+// 16-byte-chunk XOR swizzle (lds_swizzle) so that ds_read_b128 of consecutive
+// rows touches distinct bank groups.
 #include "common.h"
 #include "gemm_params.h"
 
@@ -48,15 +48,17 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group_
   tn = in_g / gs;
 }
 
-template <int BM, int BN, int EPI>
-__global__ void __launch_bounds__(256) fp8_gemm_kernel(const GemmParams p) {
+template <int BM, int BN, int WGM, int WGN, int EPI>
+__global__ void __launch_bounds__(64 * WGM * WGN) fp8_gemm_kernel(const GemmParams p) {
+  constexpr int NT = 64 * WGM * WGN;         // threads per workgroup
   constexpr int BK = 128;
-  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int MB = WM / 32, NB = WN / 32;
-  constexpr int ACH = BM * (BK / 16) / 256;  // 16-byte chunks per thread, A tile
-  constexpr int WCH = BN * (BK / 16) / 256;  // 16-byte chunks per thread, W tile
+  constexpr int ACH = BM * (BK / 16) / NT;  // 16-byte chunks per thread, A tile
+  constexpr int WCH = BN * (BK / 16) / NT;  // 16-byte chunks per thread, W tile
+  constexpr int RSTEP = NT / 8;             // rows between a thread's chunks
   constexpr int STAGE = (BM + BN) * BK;
-  static_assert(ACH >= 1 && WCH >= 1, "tile too small for 256 threads");
+  static_assert(ACH >= 1 && WCH >= 1 && MB >= 1 && NB >= 1, "tile too small");
   __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
 
   const int tiles_m = (int)((p.m + BM - 1) / BM);
@@ -68,7 +70,7 @@ __global__ void __launch_bounds__(256) fp8_gemm_kernel(const GemmParams p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave % WGM, wn = wave / WGM;
 
   // Buffer resources span only this tile's rows: every offset fits 31 bits,
   // and rows past the matrix edge read as zero.
@@ -78,78 +80,79 @@ __global__ void __launch_bounds__(256) fp8_gemm_kernel(const GemmParams p) {
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w + n0 * p.ldw, (uint32_t)(rows_w * p.ldw));
 
   const int c = tid & 7;        // 16-byte chunk of the 128-byte K slice
-  const int r0 = tid >> 3;      // rows r0 + 32 i of the tile
-  const int pc = c ^ (r0 & 7);  // swizzled chunk slot in LDS
+  const int r0 = tid >> 3;      // rows r0 + RSTEP i of the tile
+  const int pc = c ^ lds_swizzle(r0);  // swizzled chunk slot (RSTEP % 16 == 0)
   const uint32_t a_off0 = (uint32_t)(r0 * p.lda + c * 16);
   const uint32_t w_off0 = (uint32_t)(r0 * p.ldw + c * 16);
-  const uint32_t a_step = (uint32_t)(32 * p.lda), w_step = (uint32_t)(32 * p.ldw);
+  const uint32_t a_step = (uint32_t)(RSTEP * p.lda), w_step = (uint32_t)(RSTEP * p.ldw);
+  const int KT = (int)((p.k + BK - 1) / BK);
+  const int k_full = (int)(p.k / BK);  // stages with no K tail
 
   v4i va[ACH], vw[WCH];
+  // Stage kt -> registers.  Only the tail stage (uniform branch) masks chunks
+  // past K, by pointing them beyond the buffer range so they read as zero.
   auto gload = [&](int kt) {
-    const int64_t kk = (int64_t)kt * BK + c * 16;
-    const bool kin = kk < p.k;
     const uint32_t kb = (uint32_t)kt * BK;
-#pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      uint32_t off = kin ? a_off0 + i * a_step + kb : VFA_OOB;
-      va[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < WCH; ++i) {
-      uint32_t off = kin ? w_off0 + i * w_step + kb : VFA_OOB;
-      vw[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0);
+    if (kt < k_full) {
+      static_for<ACH>([&](auto i) {
+        va[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off0 + i * a_step + kb, 0, 0);
+      });
+      static_for<WCH>([&](auto i) {
+        vw[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_off0 + i * w_step + kb, 0, 0);
+      });
+    } else {
+      const uint32_t kill = ((int64_t)kb + c * 16 < p.k) ? 0u : VFA_OOB;
+      static_for<ACH>([&](auto i) {
+        va[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, (a_off0 + i * a_step + kb) | kill, 0, 0);
+      });
+      static_for<WCH>([&](auto i) {
+        vw[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, (w_off0 + i * w_step + kb) | kill, 0, 0);
+      });
     }
   };
   auto sstore = [&](int buf) {
     uint8_t* sa = smem + buf * STAGE;
     uint8_t* sw = sa + BM * BK;
-#pragma unroll
-    for (int i = 0; i < ACH; ++i)
-      *reinterpret_cast<v4i*>(sa + (r0 + 32 * i) * BK + pc * 16) = va[i];
-#pragma unroll
-    for (int i = 0; i < WCH; ++i)
-      *reinterpret_cast<v4i*>(sw + (r0 + 32 * i) * BK + pc * 16) = vw[i];
+    static_for<ACH>([&](auto i) {
+      *reinterpret_cast<v4i*>(sa + (r0 + RSTEP * i) * BK + pc * 16) = va[i];
+    });
+    static_for<WCH>([&](auto i) {
+      *reinterpret_cast<v4i*>(sw + (r0 + RSTEP * i) * BK + pc * 16) = vw[i];
+    });
   };
 
   v16f acc[NB][MB];
-#pragma unroll
-  for (int i = 0; i < NB; ++i)
-#pragma unroll
-    for (int j = 0; j < MB; ++j) acc[i][j] = v16f{};
+  static_for<NB>([&](auto i) { static_for<MB>([&](auto j) { acc[i][j] = v16f{}; }); });
 
-  const int fr = lane & 31;        // fragment row within a 32-row block
-  const int fh = lane >> 5;        // which 32-byte half of the 64-byte K step
-  const int sw7 = lane & 7;        // swizzle key (block rows start at multiples of 8)
+  const int fr = lane & 31;  // fragment row within a 32-row block
+  const int fh = lane >> 5;  // which 32-byte half of the 64-byte K step
+  const int sw7 = lds_swizzle(fr);  // block rows start at multiples of 32
   auto compute = [&](int buf) {
     const uint8_t* sa = smem + buf * STAGE + (wm * WM + fr) * BK;
     const uint8_t* sw = smem + buf * STAGE + BM * BK + (wn * WN + fr) * BK;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    static_for<2>([&](auto ks) {
       const int cc = ks * 4 + fh * 2;
       const int o0 = ((cc ^ sw7) << 4), o1 = (((cc + 1) ^ sw7) << 4);
       v8i xf[MB], wf[NB];
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
+      static_for<MB>([&](auto mb) {
         v4i lo = *reinterpret_cast<const v4i*>(sa + mb * 32 * BK + o0);
         v4i hi = *reinterpret_cast<const v4i*>(sa + mb * 32 * BK + o1);
         xf[mb] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      }
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
+      });
+      static_for<NB>([&](auto nb) {
         v4i lo = *reinterpret_cast<const v4i*>(sw + nb * 32 * BK + o0);
         v4i hi = *reinterpret_cast<const v4i*>(sw + nb * 32 * BK + o1);
         wf[nb] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      }
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
+      });
+      static_for<NB>([&](auto nb) {
+        static_for<MB>([&](auto mb) {
           acc[nb][mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
               wf[nb], xf[mb], acc[nb][mb], 0, 0, 0, 0, 0, 0);
-    }
+        });
+      });
+    });
   };
 
-  const int KT = (int)((p.k + BK - 1) / BK);
   gload(0);
   sstore(0);
   __syncthreads();
@@ -163,25 +166,18 @@ __global__ void __launch_bounds__(256) fp8_gemm_kernel(const GemmParams p) {
   // ------------------------------------------------------------------ epilogue
   // Lane holds, for block (nb, mb) and register r: row m = mb*32 + (lane & 31),
   // column n = nb*32 + 8*(r/4) + 4*(lane/32) + r%4 (relative to the wave tile).
-  float rmax[MB][NB / 2 > 0 ? NB / 2 : 1];
-  if constexpr (EPI == EPI_GELU) {
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int gi = 0; gi < (NB / 2 > 0 ? NB / 2 : 1); ++gi) rmax[mb][gi] = 0.0f;
-  }
+  constexpr int NG = NB / 2 > 0 ? NB / 2 : 1;  // 64-column groups per wave (GELU maxima)
+  float rmax[MB][NG];
+  static_for<MB>([&](auto i) { static_for<NG>([&](auto j) { rmax[i][j] = 0.0f; }); });
 
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
+  static_for<MB>([&](auto mb) {
     const int64_t m = m0 + wm * WM + mb * 32 + fr;
     const bool mvalid = m < p.m;
     const float sam = mvalid ? p.sa[m] : 0.0f;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      v16f d;
+    static_for<NB>([&](auto nb) {
+      v16f d = v16f{};
       if constexpr (EPI == EPI_LORA) {
         // delta block = B[n, :] . t[m, :] on bf16 MFMA, binary32 accumulate.
-        d = v16f{};
         const int64_t nrow = n0 + wn * WN + nb * 32 + fr;
         const bool nok = nrow < p.n;
         for (int r = 0; r < p.rank; r += 16) {
@@ -193,84 +189,85 @@ __global__ void __launch_bounds__(256) fp8_gemm_kernel(const GemmParams p) {
                                                       0);
         }
       }
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
+      static_for<4>([&](auto g) {
         const int64_t n = n0 + wn * WN + nb * 32 + g * 8 + fh * 4;
-        if (!mvalid || n >= p.n) continue;
-        float sv[4], bv[4];
+        if (mvalid && n < p.n) {
+          float sv[4], bv[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sv[i] = p.sw[n + i];
-        if (p.bias) {
-          uint2 b = *reinterpret_cast<const uint2*>(p.bias + n);
-          bv[0] = bf16_to_f32(b.x & 0xffffu);
-          bv[1] = bf16_to_f32(b.x >> 16);
-          bv[2] = bf16_to_f32(b.y & 0xffffu);
-          bv[3] = bf16_to_f32(b.y >> 16);
-        } else {
-          bv[0] = bv[1] = bv[2] = bv[3] = 0.0f;
-        }
-        uint32_t o[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float y = round_bf16(acc[nb][mb][g * 4 + i] * sam * sv[i]);
-          if (p.bias) y = round_bf16(y + bv[i]);
-          if constexpr (EPI == EPI_GELU) {
-            y = round_bf16(gelu_tanh(y));
-            rmax[mb][nb / 2] = fmaxf(rmax[mb][nb / 2], fabsf(y));
-          } else if constexpr (EPI == EPI_GATE) {
-            const float gt = bf16_to_f32(p.gate[m * p.gate_ts + (n + i) * p.gate_hs]);
-            const float res = bf16_to_f32(p.residual[m * p.ldr + n + i]);
-            y = round_bf16(res + round_bf16(gt * y));
-          } else if constexpr (EPI == EPI_LORA) {
-            float dl = round_bf16(d[g * 4 + i]);
-            if (p.lora_scale != 1.0f) dl = round_bf16(dl * p.lora_scale);
-            if (p.lora_strength != 1.0f) dl = round_bf16(dl * p.lora_strength);
-            y = round_bf16(y + dl);
+          for (int i = 0; i < 4; ++i) sv[i] = p.sw[n + i];
+          if (p.bias) {
+            uint2 b = *reinterpret_cast<const uint2*>(p.bias + n);
+            bv[0] = bf16_to_f32(b.x & 0xffffu);
+            bv[1] = bf16_to_f32(b.x >> 16);
+            bv[2] = bf16_to_f32(b.y & 0xffffu);
+            bv[3] = bf16_to_f32(b.y >> 16);
+          } else {
+            bv[0] = bv[1] = bv[2] = bv[3] = 0.0f;
           }
-          o[i] = f32_to_bf16(y);
+          uint32_t o[4];
+          static_for<4>([&](auto i) {
+            float y = round_bf16(acc[nb][mb][g * 4 + i] * sam * sv[i]);
+            if (p.bias) y = round_bf16(y + bv[i]);
+            if constexpr (EPI == EPI_GELU) {
+              y = round_bf16(gelu_tanh(y));
+              rmax[mb][nb / 2] = fmaxf(rmax[mb][nb / 2], fabsf(y));
+            } else if constexpr (EPI == EPI_GATE) {
+              const float gt = bf16_to_f32(p.gate[m * p.gate_ts + (n + i) * p.gate_hs]);
+              const float res = bf16_to_f32(p.residual[m * p.ldr + n + i]);
+              y = round_bf16(res + round_bf16(gt * y));
+            } else if constexpr (EPI == EPI_LORA) {
+              float dl = round_bf16(d[g * 4 + i]);
+              if (p.lora_scale != 1.0f) dl = round_bf16(dl * p.lora_scale);
+              if (p.lora_strength != 1.0f) dl = round_bf16(dl * p.lora_strength);
+              y = round_bf16(y + dl);
+            }
+            o[i] = f32_to_bf16(y);
+          });
+          uint16_t* dst;
+          if (p.plane_cols > 0) {
+            const int64_t plane = n / p.plane_cols;
+            dst = p.out + plane * p.plane_stride + m * p.ldo + (n - plane * p.plane_cols);
+          } else {
+            dst = p.out + m * p.ldo + n;
+          }
+          *reinterpret_cast<uint2*>(dst) =
+              make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
         }
-        uint16_t* dst;
-        if (p.plane_cols > 0) {
-          const int64_t plane = n / p.plane_cols;
-          dst = p.out + plane * p.plane_stride + m * p.ldo + (n - plane * p.plane_cols);
-        } else {
-          dst = p.out + m * p.ldo + n;
-        }
-        *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
-      }
-    }
-  }
+      });
+    });
+  });
 
   if constexpr (EPI == EPI_GELU) {
     static_assert(NB % 2 == 0, "GELU epilogue needs 64-column wave groups");
     // Lanes l and l + 32 hold the same row; each pair of 32-column blocks is
     // one 64-column group.  One partial maximum per (row, group).
     const int parts = (int)((p.n + 63) / 64);
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
+    static_for<MB>([&](auto mb) {
       const int64_t m = m0 + wm * WM + mb * 32 + fr;
-#pragma unroll
-      for (int gi = 0; gi < NB / 2; ++gi) {
-        float v = fmaxf(rmax[mb][gi], __shfl_xor(rmax[mb][gi], 32, 64));
+      static_for<NB / 2>([&](auto gi) {
+        const float v = fmaxf(rmax[mb][gi], __shfl_xor(rmax[mb][gi], 32, 64));
         const int64_t col = n0 + wn * WN + gi * 64;
         if (fh == 0 && m < p.m && col < p.n) p.amax_part[m * parts + col / 64] = v;
-      }
-    }
+      });
+    });
   }
 }
 
-template <int BM, int BN, int EPI>
+template <int BM, int BN, int WGM, int WGN, int EPI>
 static hipError_t launch_cfg(const GemmParams& p, hipStream_t s) {
   const int64_t tiles = ((p.m + BM - 1) / BM) * ((p.n + BN - 1) / BN);
-  fp8_gemm_kernel<BM, BN, EPI><<<dim3((unsigned)tiles), dim3(256), 0, s>>>(p);
+  fp8_gemm_kernel<BM, BN, WGM, WGN, EPI><<<dim3((unsigned)tiles), dim3(64 * WGM * WGN), 0, s>>>(p);
   return hipGetLastError();
 }
 
-// Tile configurations: 0 = automatic, 1 = 256x256, 2 = 128x128 (BN >= 128 for
-// GELU), 3 = 64x64, 4 = 128x256, 5 = 256x128.
+// Tile configurations (BM x BN, waves M x N): 0 = automatic,
+// 1 = 256x256 (2x2), 2 = 128x128 (2x2), 3 = 64x64 (2x2; 128x128 for GELU,
+// whose row maxima need 64-column wave groups), 4 = 128x256 (2x2),
+// 5 = 256x128 (2x2), 6 = 256x256 (4x2: two waves per SIMD),
+// 7 = 256x256 (2x4: two waves per SIMD).
 int pick_tile(const GemmParams& p) {
   auto tiles = [&](int bm, int bn) { return ((p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn); };
-  if (tiles(256, 256) >= 512) return 1;
+  if (tiles(256, 256) >= 512) return 6;
   if (tiles(128, 128) >= 256) return 2;
   return 3;
 }
@@ -278,13 +275,15 @@ int pick_tile(const GemmParams& p) {
 template <int EPI>
 hipError_t launch_epi(const GemmParams& p, int tile, hipStream_t s) {
   switch (tile) {
-    case 1: return launch_cfg<256, 256, EPI>(p, s);
-    case 2: return launch_cfg<128, 128, EPI>(p, s);
+    case 1: return launch_cfg<256, 256, 2, 2, EPI>(p, s);
+    case 2: return launch_cfg<128, 128, 2, 2, EPI>(p, s);
     case 3:
-      if constexpr (EPI == EPI_GELU) return launch_cfg<128, 128, EPI>(p, s);
-      else return launch_cfg<64, 64, EPI>(p, s);
-    case 4: return launch_cfg<128, 256, EPI>(p, s);
-    case 5: return launch_cfg<256, 128, EPI>(p, s);
+      if constexpr (EPI == EPI_GELU) return launch_cfg<128, 128, 2, 2, EPI>(p, s);
+      else return launch_cfg<64, 64, 2, 2, EPI>(p, s);
+    case 4: return launch_cfg<128, 256, 2, 2, EPI>(p, s);
+    case 5: return launch_cfg<256, 128, 2, 2, EPI>(p, s);
+    case 6: return launch_cfg<256, 256, 4, 2, EPI>(p, s);
+    case 7: return launch_cfg<256, 256, 2, 4, EPI>(p, s);
     default: return hipErrorInvalidValue;
   }
 }

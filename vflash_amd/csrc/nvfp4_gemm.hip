@@ -107,7 +107,7 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_kernel(const Fp4Params p) {
       }
     }
   };
-  // LDS rows hold 64 bf16 = 8 chunks of 16 bytes, chunk slot swizzled by row & 7.
+  // LDS rows hold 64 bf16 = 8 chunks of 16 bytes, slots swizzled by lds_swizzle(row).
   auto sstore = [&](int buf) {
     uint8_t* sa = smem + buf * STAGE;
     uint8_t* sw = sa + BM * ROWB;
@@ -122,9 +122,9 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_kernel(const Fp4Params p) {
         h[2 * j + 1] = pack_exact_bf16(e4m3_to_f32((wd >> 16) & 0xff), e4m3_to_f32(wd >> 24));
       }
       const int c0 = ac * 2;  // two 16-byte chunks: 16 codes -> 16 bf16
-      *reinterpret_cast<v4i*>(sa + row * ROWB + ((c0 ^ (row & 7)) << 4)) =
+      *reinterpret_cast<v4i*>(sa + row * ROWB + ((c0 ^ lds_swizzle(row)) << 4)) =
           v4i{(int)h[0], (int)h[1], (int)h[2], (int)h[3]};
-      *reinterpret_cast<v4i*>(sa + row * ROWB + (((c0 + 1) ^ (row & 7)) << 4)) =
+      *reinterpret_cast<v4i*>(sa + row * ROWB + (((c0 + 1) ^ lds_swizzle(row)) << 4)) =
           v4i{(int)h[4], (int)h[5], (int)h[6], (int)h[7]};
     }
 #pragma unroll
@@ -144,9 +144,9 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_kernel(const Fp4Params p) {
           }
         }
         const int c0 = wc * 4 + half * 2;
-        *reinterpret_cast<v4i*>(sw + row * ROWB + ((c0 ^ (row & 7)) << 4)) =
+        *reinterpret_cast<v4i*>(sw + row * ROWB + ((c0 ^ lds_swizzle(row)) << 4)) =
             v4i{(int)h[0], (int)h[1], (int)h[2], (int)h[3]};
-        *reinterpret_cast<v4i*>(sw + row * ROWB + (((c0 + 1) ^ (row & 7)) << 4)) =
+        *reinterpret_cast<v4i*>(sw + row * ROWB + (((c0 + 1) ^ lds_swizzle(row)) << 4)) =
             v4i{(int)h[4], (int)h[5], (int)h[6], (int)h[7]};
       }
     }
@@ -158,7 +158,7 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_kernel(const Fp4Params p) {
 #pragma unroll
     for (int j = 0; j < MB; ++j) acc[i][j] = v16f{};
 
-  const int fr = lane & 31, fh = lane >> 5, sw7 = lane & 7;
+  const int fr = lane & 31, fh = lane >> 5, sw7 = lds_swizzle(fr);
   auto compute = [&](int buf) {
     const uint8_t* sa = smem + buf * STAGE + (wm * WM + fr) * ROWB;
     const uint8_t* sw = smem + buf * STAGE + BM * ROWB + (wn * WN + fr) * ROWB;

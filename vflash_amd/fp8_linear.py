@@ -34,15 +34,21 @@ def _quantize_activation_torch(matrix):
     Same arithmetic as h3_fp8_linear.py:18-31 (and the HIP kernel): fp32 row
     maximum, ``scale = max(amax / 448, FLT_MIN)`` (1 for a zero row), codes
     ``e4m3(clamp(x / scale, -448, 448))``.
+
+    The divisor 448 is a device tensor, not a Python scalar: torch's GPU
+    kernels compute ``tensor / python_scalar`` as a multiplication by the
+    reciprocal, which differs from IEEE division (used by the fused kernel's
+    ``div_rn`` and by this expression on the CPU) in about half of all inputs.
     """
     rows = matrix.shape[0]
     if rows % 16:
         matrix = torch.nn.functional.pad(matrix, (0, 0, 0, 16 - rows % 16))
     floats = matrix.float()
     maxima = floats.abs().amax(dim=1, keepdim=True)
+    limit = torch.full((), 448.0, dtype=torch.float32, device=floats.device)
     act_scale = torch.where(
         maxima > 0,
-        (maxima / 448.0).clamp_min(torch.finfo(torch.float32).tiny),
+        (maxima / limit).clamp_min(torch.finfo(torch.float32).tiny),
         torch.ones_like(maxima),
     )
     codes = (floats / act_scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)

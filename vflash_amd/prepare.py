@@ -30,7 +30,9 @@ def quantize_weight_rows(weight: torch.Tensor):
     """E4M3 codes [N, K] and fp32 row scales [N, 1] of a real weight matrix."""
     floats = weight.float()
     maxima = floats.abs().amax(dim=1, keepdim=True)
-    scale = torch.where(maxima > 0, (maxima / 448.0).clamp_min(FLT_MIN), torch.ones_like(maxima))
+    # A tensor divisor keeps IEEE division on every device (see _quantize_activation_torch).
+    limit = torch.full((), 448.0, dtype=torch.float32, device=floats.device)
+    scale = torch.where(maxima > 0, (maxima / limit).clamp_min(FLT_MIN), torch.ones_like(maxima))
     codes = (floats / scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
     return codes, scale
 
