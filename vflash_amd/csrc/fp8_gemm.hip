@@ -48,6 +48,153 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group_
   tn = in_g / gs;
 }
 
+// Epilogue shared by every tiling, in two phases through LDS.
+//
+// Phase 1 (per wave, from the accumulators): a lane holds, for 32x32 block
+// (nb, mb) and register r, tile row mb*32 + (lane & 31) and tile column
+// nb*32 + 8*(r/4) + 4*(lane/32) + r%4 of its wave's sub-tile.  It applies the
+// scales, bias and the register-level epilogue (GELU, LoRA merge), rounds to
+// bf16 and writes the values into a BM x BN bf16 staging tile in LDS (16-byte
+// chunk c of row r stored in slot c ^ (r % chunks-per-row)).  Scale and bias
+// vectors are loaded once, before any store.
+// Phase 2 (whole workgroup): each thread moves 16-byte row chunks from LDS to
+// global memory with coalesced 16-byte stores, applying the gate-residual
+// epilogue there with coalesced residual loads.
+template <int BM, int BN, int WGM, int WGN, int EPI>
+__device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
+                                              v16f (&acc)[BN / WGN / 32][BM / WGM / 32],
+                                              int64_t m0, int64_t n0, int wm, int wn, int tid,
+                                              uint8_t* stage) {
+  constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
+  constexpr int NT = 64 * WGM * WGN;
+  constexpr int CH = BN / 8;  // 16-byte chunks per staged row
+  constexpr int PITCH = BN * 2;
+  const int lane = tid & 63, fr = lane & 31, fh = lane >> 5;
+  const float* __restrict__ sa_p = p.sa;
+  const float* __restrict__ sw_p = p.sw;
+  const uint16_t* __restrict__ bias_p = p.bias;
+
+  constexpr int NG = NB / 2 > 0 ? NB / 2 : 1;  // 64-column groups per wave (GELU maxima)
+  float rmax[MB][NG];
+  static_for<MB>([&](auto i) { static_for<NG>([&](auto j) { rmax[i][j] = 0.0f; }); });
+  float sam[MB];
+  static_for<MB>([&](auto mb) {
+    const int64_t m = m0 + wm * WM + mb * 32 + fr;
+    sam[mb] = m < p.m ? sa_p[m] : 0.0f;
+  });
+
+  // Column-block major: the scale and bias of one 32-column block (4 columns
+  // per g for this lane) are live while its MB row blocks are written.  All
+  // phase-1 stores go to LDS, so these global loads never wait on them.
+  static_for<NB>([&](auto nb) {
+    float sv[4][4], bv[4][4];
+    static_for<4>([&](auto g) {
+      const int64_t n = n0 + wn * WN + nb * 32 + g * 8 + fh * 4;
+      const bool ok = n < p.n;
+      static_for<4>([&](auto i) {
+        sv[g][i] = ok ? sw_p[n + i] : 0.0f;
+        bv[g][i] = (ok && bias_p) ? bf16_to_f32(bias_p[n + i]) : 0.0f;
+      });
+    });
+    static_for<MB>([&](auto mb) {
+      const int row = wm * WM + mb * 32 + fr;  // tile row
+      const int64_t m = m0 + row;
+      const bool mvalid = m < p.m;
+      v16f d = v16f{};
+      if constexpr (EPI == EPI_LORA) {
+        // delta block = B[n, :] . t[m, :] on bf16 MFMA, binary32 accumulate.
+        const int64_t nrow = n0 + wn * WN + nb * 32 + fr;
+        const bool nok = nrow < p.n;
+        for (int r = 0; r < p.rank; r += 16) {
+          v8s bfr = v8s{}, tfr = v8s{};
+          if (nok) bfr = *reinterpret_cast<const v8s*>(p.lora_b + nrow * p.ldb + r + fh * 8);
+          if (mvalid) tfr = *reinterpret_cast<const v8s*>(p.lora_t + m * p.ldt + r + fh * 8);
+          d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, bfr),
+                                                      __builtin_bit_cast(v8bf, tfr), d, 0, 0,
+                                                      0);
+        }
+      }
+      static_for<4>([&](auto g) {
+        uint32_t w[2];
+        // Output pairs: every bf16 rounding is one v_cvt_pk_bf16_f32 for two values.
+        static_for<2>([&](auto h) {
+          constexpr int i0 = 2 * h, i1 = 2 * h + 1;
+          uint32_t pw = pack_bf16x2(acc[nb][mb][g * 4 + i0] * sam[mb] * sv[g][i0],
+                                    acc[nb][mb][g * 4 + i1] * sam[mb] * sv[g][i1]);
+          if (bias_p) pw = pack_bf16x2(bf16_lo(pw) + bv[g][i0], bf16_hi(pw) + bv[g][i1]);
+          if constexpr (EPI == EPI_GELU) {
+            pw = pack_bf16x2(gelu_tanh(bf16_lo(pw)), gelu_tanh(bf16_hi(pw)));
+            rmax[mb][nb / 2] =
+                fmaxf(rmax[mb][nb / 2], fmaxf(fabsf(bf16_lo(pw)), fabsf(bf16_hi(pw))));
+          } else if constexpr (EPI == EPI_LORA) {
+            uint32_t dp = pack_bf16x2(d[g * 4 + i0], d[g * 4 + i1]);
+            if (p.lora_scale != 1.0f)
+              dp = pack_bf16x2(bf16_lo(dp) * p.lora_scale, bf16_hi(dp) * p.lora_scale);
+            if (p.lora_strength != 1.0f)
+              dp = pack_bf16x2(bf16_lo(dp) * p.lora_strength, bf16_hi(dp) * p.lora_strength);
+            pw = pack_bf16x2(bf16_lo(pw) + bf16_lo(dp), bf16_hi(pw) + bf16_hi(dp));
+          }
+          w[h] = pw;
+        });
+        const int c = (wn * WN + nb * 32 + g * 8) / 8;  // 16-byte chunk of the row
+        *reinterpret_cast<uint2*>(stage + row * PITCH + ((c ^ (row % CH)) << 4) + fh * 8) =
+            make_uint2(w[0], w[1]);
+      });
+    });
+  });
+
+  if constexpr (EPI == EPI_GELU) {
+    static_assert(NB % 2 == 0, "GELU epilogue needs 64-column wave groups");
+    // Lanes l and l + 32 hold the same row; each pair of 32-column blocks is
+    // one 64-column group.  One partial maximum per (row, group).
+    const int parts = (int)((p.n + 63) / 64);
+    static_for<MB>([&](auto mb) {
+      const int64_t m = m0 + wm * WM + mb * 32 + fr;
+      static_for<NB / 2>([&](auto gi) {
+        const float v = fmaxf(rmax[mb][gi], __shfl_xor(rmax[mb][gi], 32, 64));
+        const int64_t col = n0 + wn * WN + gi * 64;
+        if (fh == 0 && m < p.m && col < p.n) p.amax_part[m * parts + col / 64] = v;
+      });
+    });
+  }
+  __syncthreads();
+
+  // Phase 2: LDS rows -> global, 16 bytes per thread per step.
+  const bool vec_out = ((reinterpret_cast<uintptr_t>(p.out) & 15) == 0) && (p.ldo % 8 == 0) &&
+                       (p.plane_cols == 0 || p.plane_stride % 8 == 0);
+  for (int q = tid; q < BM * CH; q += NT) {
+    const int row = q / CH, c = q % CH;
+    const int64_t m = m0 + row, n = n0 + c * 8;
+    if (m >= p.m || n >= p.n) continue;
+    v4i v = *reinterpret_cast<const v4i*>(stage + row * PITCH + ((c ^ (row % CH)) << 4));
+    if constexpr (EPI == EPI_GATE) {
+      const uint16_t* res = p.residual + m * p.ldr + n;
+      const uint16_t* gt = p.gate + m * p.gate_ts + n * p.gate_hs;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t y = (uint32_t)v[j];
+        const uint32_t gy = pack_bf16x2(bf16_to_f32(gt[(2 * j) * p.gate_hs]) * bf16_lo(y),
+                                        bf16_to_f32(gt[(2 * j + 1) * p.gate_hs]) * bf16_hi(y));
+        v[j] = (int)pack_bf16x2(bf16_to_f32(res[2 * j]) + bf16_lo(gy),
+                                bf16_to_f32(res[2 * j + 1]) + bf16_hi(gy));
+      }
+    }
+    uint16_t* dst;
+    if (p.plane_cols > 0) {
+      const int64_t plane = n / p.plane_cols;
+      dst = p.out + plane * p.plane_stride + m * p.ldo + (n - plane * p.plane_cols);
+    } else {
+      dst = p.out + m * p.ldo + n;
+    }
+    if (vec_out) {
+      *reinterpret_cast<v4i*>(dst) = v;
+    } else {
+      reinterpret_cast<uint2*>(dst)[0] = make_uint2((uint32_t)v[0], (uint32_t)v[1]);
+      reinterpret_cast<uint2*>(dst)[1] = make_uint2((uint32_t)v[2], (uint32_t)v[3]);
+    }
+  }
+}
+
 template <int BM, int BN, int WGM, int WGN, int EPI>
 __global__ void __launch_bounds__(64 * WGM * WGN) fp8_gemm_kernel(const GemmParams p) {
   constexpr int NT = 64 * WGM * WGN;         // threads per workgroup
@@ -163,94 +310,144 @@ __global__ void __launch_bounds__(64 * WGM * WGN) fp8_gemm_kernel(const GemmPara
     __syncthreads();
   }
 
-  // ------------------------------------------------------------------ epilogue
-  // Lane holds, for block (nb, mb) and register r: row m = mb*32 + (lane & 31),
-  // column n = nb*32 + 8*(r/4) + 4*(lane/32) + r%4 (relative to the wave tile).
-  constexpr int NG = NB / 2 > 0 ? NB / 2 : 1;  // 64-column groups per wave (GELU maxima)
-  float rmax[MB][NG];
-  static_for<MB>([&](auto i) { static_for<NG>([&](auto j) { rmax[i][j] = 0.0f; }); });
+  gemm_epilogue<BM, BN, WGM, WGN, EPI>(p, acc, m0, n0, wm, wn, tid, smem);
+}
 
-  static_for<MB>([&](auto mb) {
-    const int64_t m = m0 + wm * WM + mb * 32 + fr;
-    const bool mvalid = m < p.m;
-    const float sam = mvalid ? p.sa[m] : 0.0f;
-    static_for<NB>([&](auto nb) {
-      v16f d = v16f{};
-      if constexpr (EPI == EPI_LORA) {
-        // delta block = B[n, :] . t[m, :] on bf16 MFMA, binary32 accumulate.
-        const int64_t nrow = n0 + wn * WN + nb * 32 + fr;
-        const bool nok = nrow < p.n;
-        for (int r = 0; r < p.rank; r += 16) {
-          v8s bfr = v8s{}, tfr = v8s{};
-          if (nok) bfr = *reinterpret_cast<const v8s*>(p.lora_b + nrow * p.ldb + r + fh * 8);
-          if (mvalid) tfr = *reinterpret_cast<const v8s*>(p.lora_t + m * p.ldt + r + fh * 8);
-          d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, bfr),
-                                                      __builtin_bit_cast(v8bf, tfr), d, 0, 0,
-                                                      0);
-        }
-      }
-      static_for<4>([&](auto g) {
-        const int64_t n = n0 + wn * WN + nb * 32 + g * 8 + fh * 4;
-        if (mvalid && n < p.n) {
-          float sv[4], bv[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) sv[i] = p.sw[n + i];
-          if (p.bias) {
-            uint2 b = *reinterpret_cast<const uint2*>(p.bias + n);
-            bv[0] = bf16_to_f32(b.x & 0xffffu);
-            bv[1] = bf16_to_f32(b.x >> 16);
-            bv[2] = bf16_to_f32(b.y & 0xffffu);
-            bv[3] = bf16_to_f32(b.y >> 16);
-          } else {
-            bv[0] = bv[1] = bv[2] = bv[3] = 0.0f;
-          }
-          uint32_t o[4];
-          static_for<4>([&](auto i) {
-            float y = round_bf16(acc[nb][mb][g * 4 + i] * sam * sv[i]);
-            if (p.bias) y = round_bf16(y + bv[i]);
-            if constexpr (EPI == EPI_GELU) {
-              y = round_bf16(gelu_tanh(y));
-              rmax[mb][nb / 2] = fmaxf(rmax[mb][nb / 2], fabsf(y));
-            } else if constexpr (EPI == EPI_GATE) {
-              const float gt = bf16_to_f32(p.gate[m * p.gate_ts + (n + i) * p.gate_hs]);
-              const float res = bf16_to_f32(p.residual[m * p.ldr + n + i]);
-              y = round_bf16(res + round_bf16(gt * y));
-            } else if constexpr (EPI == EPI_LORA) {
-              float dl = round_bf16(d[g * 4 + i]);
-              if (p.lora_scale != 1.0f) dl = round_bf16(dl * p.lora_scale);
-              if (p.lora_strength != 1.0f) dl = round_bf16(dl * p.lora_strength);
-              y = round_bf16(y + dl);
-            }
-            o[i] = f32_to_bf16(y);
-          });
-          uint16_t* dst;
-          if (p.plane_cols > 0) {
-            const int64_t plane = n / p.plane_cols;
-            dst = p.out + plane * p.plane_stride + m * p.ldo + (n - plane * p.plane_cols);
-          } else {
-            dst = p.out + m * p.ldo + n;
-          }
-          *reinterpret_cast<uint2*>(dst) =
-              make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
-        }
-      });
-    });
+// ---------------------------------------------------------------------------
+// Pipelined 256x256 main loop.
+//
+// K advances 64 bytes per stage.  A ring of NS = 4 LDS stages (32 KB each:
+// A and W halves of 256 rows x 64 bytes) is filled by buffer-load-to-LDS DMA
+// (buffer_load_dwordx4 ... lds), issued NS - 1 stages ahead of the stage being
+// multiplied, so global latency is covered by three stages of MFMA work and no
+// VGPRs are spent on staging.  The DMA is issued as inline assembly, so the
+// waits below are the only ones that order it against the fragment reads.
+// Per stage:
+//   wait for this wave's DMA of stage kt+1 and its own LDS reads, s_barrier;
+//   issue the DMA of stage kt+NS into the slot just consumed;
+//   run the MFMAs of stage kt from registers while reading the fragments of
+//   stage kt+1 from LDS into the other register set.
+// LDS rows are 64 bytes (four 16-byte chunks); chunk c of row r sits in slot
+// c ^ ((r >> 2) & 3), which keeps the 16 rows of one ds_read_b128 pass on
+// distinct bank groups of the 256-byte-wide LDS.
+template <int WGM, int WGN, int EPI>
+__global__ void __launch_bounds__(64 * WGM * WGN) fp8_gemm_pipe(const GemmParams p) {
+  constexpr int BM = 256, BN = 256, BK = 64, NS = 4;
+  constexpr int NW = WGM * WGN;
+  constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
+  constexpr int HALF = BM * BK;                // bytes of one operand per stage
+  constexpr int DMA_A = HALF / 1024 / NW;      // 1 KB DMA instructions per wave
+  constexpr int DMA = 2 * DMA_A;               // per wave per stage (A and W)
+  static_assert(DMA_A >= 1 && NS % 2 == 0, "ring shape");
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * 2 * HALF];
+  static_assert(NS * 2 * HALF >= BM * BN * 2, "the ring doubles as the epilogue staging tile");
+  auto slot = [&](auto j) -> uint8_t* { return ring + j * 2 * HALF; };
+
+  const int tiles_m = (int)((p.m + BM - 1) / BM);
+  const int tiles_n = (int)((p.n + BN - 1) / BN);
+  int tm, tn;
+  tile_coords(tiles_m, tiles_n, p.group_m, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave % WGM, wn = wave / WGM;
+
+  const int64_t rows_a = min((int64_t)BM, p.m - m0);
+  const int64_t rows_w = min((int64_t)BN, p.n - n0);
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + m0 * p.lda, (uint32_t)(rows_a * p.lda));
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w + n0 * p.ldw, (uint32_t)(rows_w * p.ldw));
+
+  // DMA lane map: block b (1 KB) of an operand holds rows 16b..16b+15; lane l
+  // fills row 16b + l/4, slot l%4, from logical chunk (l%4) ^ swizzle(row).
+  const int drow = lane >> 2;
+  const int dchunk = (lane & 3) ^ ((drow >> 2) & 3);
+  uint32_t a_off[DMA_A], w_off[DMA_A];
+  static_for<DMA_A>([&](auto j) {
+    const int row = (wave * DMA_A + j) * 16 + drow;
+    a_off[j] = (uint32_t)(row * p.lda + dchunk * 16);
+    w_off[j] = (uint32_t)(row * p.ldw + dchunk * 16);
   });
+  const int KT = (int)((p.k + BK - 1) / BK);
 
-  if constexpr (EPI == EPI_GELU) {
-    static_assert(NB % 2 == 0, "GELU epilogue needs 64-column wave groups");
-    // Lanes l and l + 32 hold the same row; each pair of 32-column blocks is
-    // one 64-column group.  One partial maximum per (row, group).
-    const int parts = (int)((p.n + 63) / 64);
-    static_for<MB>([&](auto mb) {
-      const int64_t m = m0 + wm * WM + mb * 32 + fr;
-      static_for<NB / 2>([&](auto gi) {
-        const float v = fmaxf(rmax[mb][gi], __shfl_xor(rmax[mb][gi], 32, 64));
-        const int64_t col = n0 + wn * WN + gi * 64;
-        if (fh == 0 && m < p.m && col < p.n) p.amax_part[m * parts + col / 64] = v;
-      });
+  // DMA of stage s into ring slot j; chunks at or past K (including whole
+  // stages past the end) are pointed beyond the buffer and arrive as zeros.
+  auto issue = [&](auto j, int s) {
+    uint8_t* base = slot(j);
+    const int64_t kk = (int64_t)s * BK + dchunk * 16;
+    const uint32_t kill = kk < p.k ? 0u : VFA_OOB;
+    const uint32_t kb = (uint32_t)s * BK;
+    static_for<DMA_A>([&](auto i) {
+      lds_dma16(ra, base + (wave * DMA_A + i) * 1024, (a_off[i] + kb) | kill);
+    });
+    static_for<DMA_A>([&](auto i) {
+      lds_dma16(rw, base + HALF + (wave * DMA_A + i) * 1024, (w_off[i] + kb) | kill);
+    });
+  };
+
+  const int fr = lane & 31, fh = lane >> 5;
+  const int fsw = (fr >> 2) & 3;
+  const int o0 = ((fh * 2) ^ fsw) << 4, o1 = ((fh * 2 + 1) ^ fsw) << 4;
+  v8i F[2][MB + NB];  // fragment sets: [0, MB) activation blocks, [MB, MB+NB) weight blocks
+  auto read = [&](auto j, auto fb) {
+    const uint8_t* sa = slot(j) + (wm * WM + fr) * BK;
+    const uint8_t* sw = slot(j) + HALF + (wn * WN + fr) * BK;
+    static_for<MB + NB>([&](auto f) {
+      const uint8_t* src = f < MB ? sa + f * 32 * BK : sw + (f - MB) * 32 * BK;
+      const v4i lo = *reinterpret_cast<const v4i*>(src + o0);
+      const v4i hi = *reinterpret_cast<const v4i*>(src + o1);
+      F[fb][f] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    });
+  };
+
+  v16f acc[NB][MB];
+  static_for<NB>([&](auto i) { static_for<MB>([&](auto jj) { acc[i][jj] = v16f{}; }); });
+
+  // Wait until at most n of this wave's newest DMAs are in flight and its own
+  // LDS reads are done, then meet the other waves.
+  auto wait_stage = [&](auto inflight) {
+    wait_vmcnt<decltype(inflight)::value, true>();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  static_for<NS>([&](auto j) { issue(j, (int)j); });
+  wait_stage(std::integral_constant<int, DMA * (NS - 1)>{});
+  read(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+
+  for (int kt0 = 0; kt0 < KT; kt0 += NS) {
+    static_for<NS>([&](auto j) {
+      const int kt = kt0 + j;
+      if (kt < KT) {
+        constexpr int fb = j % 2;
+        wait_stage(std::integral_constant<int, DMA * (NS - 2)>{});
+        issue(j, kt + NS);
+        static_for<NB>([&](auto nb) {
+          static_for<MB>([&](auto mb) {
+            acc[nb][mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                F[fb][MB + nb], F[fb][mb], acc[nb][mb], 0, 0, 0, 0, 0, 0);
+          });
+        });
+        // Fragments of stage kt+1 (slot contents are unused after the last stage).
+        read(std::integral_constant<int, (j + 1) % NS>{}, std::integral_constant<int, 1 - fb>{});
+        // One fragment read after each MFMA while the MFMA pipe is busy.
+        static_for<(MB * NB < 2 * (MB + NB) ? MB * NB : 2 * (MB + NB))>([&](auto) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        });
+      }
     });
   }
+  wait_vmcnt<0, true>();  // every ring DMA has landed before the ring is reused
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  gemm_epilogue<BM, BN, WGM, WGN, EPI>(p, acc, m0, n0, wm, wn, (int)threadIdx.x, ring);
+}
+
+template <int WGM, int WGN, int EPI>
+static hipError_t launch_pipe(const GemmParams& p, hipStream_t s) {
+  const int64_t tiles = ((p.m + 255) / 256) * ((p.n + 255) / 256);
+  fp8_gemm_pipe<WGM, WGN, EPI><<<dim3((unsigned)tiles), dim3(64 * WGM * WGN), 0, s>>>(p);
+  return hipGetLastError();
 }
 
 template <int BM, int BN, int WGM, int WGN, int EPI>
@@ -264,7 +461,8 @@ static hipError_t launch_cfg(const GemmParams& p, hipStream_t s) {
 // 1 = 256x256 (2x2), 2 = 128x128 (2x2), 3 = 64x64 (2x2; 128x128 for GELU,
 // whose row maxima need 64-column wave groups), 4 = 128x256 (2x2),
 // 5 = 256x128 (2x2), 6 = 256x256 (4x2: two waves per SIMD),
-// 7 = 256x256 (2x4: two waves per SIMD).
+// 7 = 256x256 (2x4: two waves per SIMD), 8 = 256x256 pipelined (2x2),
+// 9 = 256x256 pipelined (2x4).
 int pick_tile(const GemmParams& p) {
   auto tiles = [&](int bm, int bn) { return ((p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn); };
   if (tiles(256, 256) >= 512) return 6;
@@ -284,6 +482,8 @@ hipError_t launch_epi(const GemmParams& p, int tile, hipStream_t s) {
     case 5: return launch_cfg<256, 128, 2, 2, EPI>(p, s);
     case 6: return launch_cfg<256, 256, 4, 2, EPI>(p, s);
     case 7: return launch_cfg<256, 256, 2, 4, EPI>(p, s);
+    case 8: return launch_pipe<2, 2, EPI>(p, s);
+    case 9: return launch_pipe<2, 4, EPI>(p, s);
     default: return hipErrorInvalidValue;
   }
 }
