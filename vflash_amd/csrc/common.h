@@ -107,20 +107,27 @@ __device__ __forceinline__ int lds_swizzle(int row) { return (row ^ ((row >> 3) 
 // An offset that is always past num_records (num_records < 2^31 by construction).
 #define VFA_OOB 0x80000000u
 
+// LDS byte address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
 // Wave-wide buffer load straight into LDS (buffer_load_dwordx4 ... lds): the
-// 16 bytes lane l reads at `voffset` land at lds_dst + 16 * l, where lds_dst
-// is the same for the whole wave.  Out-of-range offsets deliver zeros.  It is
-// written as inline assembly so that the compiler inserts no waits for it:
-// the caller waits with vmcnt (and a barrier for other waves' loads) before
-// it reads the destination, and must not let the kernel end with one pending.
-__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, const void* lds_dst,
+// 16 bytes lane l reads at `voffset` land at LDS byte address lds_dst + 16 * l,
+// where lds_dst (wave-uniform) is an address from lds_addr().  Out-of-range
+// offsets deliver zeros.  It is written as inline assembly so that the
+// compiler inserts no waits for it: the caller waits with vmcnt (and a barrier
+// for other waves' loads) before it reads the destination, and must not let
+// the kernel end with one pending.  The statement has no memory clobber, so
+// LDS reads of other buffers may be scheduled around it; ordering against
+// reads of the destination comes from the caller's barrier, which is fenced
+// by "memory"-clobbering volatile statements that volatile DMAs never cross.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint32_t lds_dst,
                                           uint32_t voffset) {
-  const uint32_t base = __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds_dst);
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
-               : "s"(base), "v"(voffset), "s"(r)
-               : "memory", "m0");
+               : "s"(__builtin_amdgcn_readfirstlane(lds_dst)), "v"(voffset), "s"(r)
+               : "m0");
 }
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:

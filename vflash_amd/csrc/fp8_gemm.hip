@@ -316,7 +316,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) fp8_gemm_kernel(const GemmPara
 // ---------------------------------------------------------------------------
 // Pipelined 256x256 main loop.
 //
-// K advances 64 bytes per stage.  A ring of NS = 4 LDS stages (32 KB each:
+// K advances 64 bytes per stage.  A ring of NS = 5 LDS stages (32 KB each:
 // A and W halves of 256 rows x 64 bytes) is filled by buffer-load-to-LDS DMA
 // (buffer_load_dwordx4 ... lds), issued NS - 1 stages ahead of the stage being
 // multiplied, so global latency is covered by three stages of MFMA work and no
@@ -332,16 +332,18 @@ __global__ void __launch_bounds__(64 * WGM * WGN) fp8_gemm_kernel(const GemmPara
 // distinct bank groups of the 256-byte-wide LDS.
 template <int WGM, int WGN, int EPI>
 __global__ void __launch_bounds__(64 * WGM * WGN) fp8_gemm_pipe(const GemmParams p) {
-  constexpr int BM = 256, BN = 256, BK = 64, NS = 4;
+  constexpr int BM = 256, BN = 256, BK = 64, NS = 5;
+  constexpr int UN = NS % 2 ? 2 * NS : NS;  // unroll: ring slot and fragment set both static
   constexpr int NW = WGM * WGN;
   constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
   constexpr int HALF = BM * BK;                // bytes of one operand per stage
   constexpr int DMA_A = HALF / 1024 / NW;      // 1 KB DMA instructions per wave
   constexpr int DMA = 2 * DMA_A;               // per wave per stage (A and W)
-  static_assert(DMA_A >= 1 && NS % 2 == 0, "ring shape");
+  static_assert(DMA_A >= 1 && NS >= 3, "ring shape");
   __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * 2 * HALF];
   static_assert(NS * 2 * HALF >= BM * BN * 2, "the ring doubles as the epilogue staging tile");
   auto slot = [&](auto j) -> uint8_t* { return ring + j * 2 * HALF; };
+  const uint32_t ring_lds = lds_addr(ring);
 
   const int tiles_m = (int)((p.m + BM - 1) / BM);
   const int tiles_n = (int)((p.n + BN - 1) / BN);
@@ -370,16 +372,15 @@ __global__ void __launch_bounds__(64 * WGM * WGN) fp8_gemm_pipe(const GemmParams
 
   // DMA of stage s into ring slot j; chunks at or past K (including whole
   // stages past the end) are pointed beyond the buffer and arrive as zeros.
+  const uint32_t wave_lds = ring_lds + wave * DMA_A * 1024;
   auto issue = [&](auto j, int s) {
-    uint8_t* base = slot(j);
+    const uint32_t base = wave_lds + j * 2 * HALF;
     const int64_t kk = (int64_t)s * BK + dchunk * 16;
     const uint32_t kill = kk < p.k ? 0u : VFA_OOB;
     const uint32_t kb = (uint32_t)s * BK;
+    static_for<DMA_A>([&](auto i) { lds_dma16(ra, base + i * 1024, (a_off[i] + kb) | kill); });
     static_for<DMA_A>([&](auto i) {
-      lds_dma16(ra, base + (wave * DMA_A + i) * 1024, (a_off[i] + kb) | kill);
-    });
-    static_for<DMA_A>([&](auto i) {
-      lds_dma16(rw, base + HALF + (wave * DMA_A + i) * 1024, (w_off[i] + kb) | kill);
+      lds_dma16(rw, base + HALF + i * 1024, (w_off[i] + kb) | kill);
     });
   };
 
@@ -414,13 +415,13 @@ __global__ void __launch_bounds__(64 * WGM * WGN) fp8_gemm_pipe(const GemmParams
   wait_stage(std::integral_constant<int, DMA * (NS - 1)>{});
   read(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
 
-  for (int kt0 = 0; kt0 < KT; kt0 += NS) {
-    static_for<NS>([&](auto j) {
-      const int kt = kt0 + j;
+  for (int kt0 = 0; kt0 < KT; kt0 += UN) {
+    static_for<UN>([&](auto u) {
+      const int kt = kt0 + u;
       if (kt < KT) {
-        constexpr int fb = j % 2;
+        constexpr int j = u % NS, fb = u % 2;
         wait_stage(std::integral_constant<int, DMA * (NS - 2)>{});
-        issue(j, kt + NS);
+        issue(std::integral_constant<int, j>{}, kt + NS);
         static_for<NB>([&](auto nb) {
           static_for<MB>([&](auto mb) {
             acc[nb][mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
@@ -443,6 +444,167 @@ __global__ void __launch_bounds__(64 * WGM * WGN) fp8_gemm_pipe(const GemmParams
   gemm_epilogue<BM, BN, WGM, WGN, EPI>(p, acc, m0, n0, wm, wn, (int)threadIdx.x, ring);
 }
 
+// ---------------------------------------------------------------------------
+// Two-slot pipelined 256x256 main loop with 128-byte K stages.
+//
+// Each stage holds 128 bytes of K for all 256 A rows and 256 W rows (64 KB);
+// two LDS slots alternate.  The DMA reads whole 128-byte row segments (eight
+// lanes per row), which moves L2 data into LDS markedly faster than 64-byte
+// segments.  Per stage kt, per wave (2x2 waves, 128x128 each):
+//   16 MFMAs of K-substep 0, interleaved with the LDS reads of substep 1;
+//   8 MFMAs of substep 1;
+//   wait for this wave's DMA of stage kt+1 and its own LDS reads, s_barrier;
+//   issue the DMA of stage kt+2 into the slot of stage kt (fully read now);
+//   8 MFMAs of substep 1, interleaved with the reads of stage kt+1 substep 0.
+// The DMA of a stage is issued about one stage of MFMA work before it is
+// needed; rows are stored with the lds_swizzle chunk permutation.
+template <int EPI>
+__global__ void __launch_bounds__(256) fp8_gemm_pipe2(const GemmParams p) {
+  constexpr int BM = 256, BN = 256, BK = 128, WGM = 2, WGN = 2;
+  constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
+  constexpr int HALF = BM * BK;            // 32 KB: one operand of one stage
+  constexpr int SLOT = 2 * HALF;           // 64 KB
+  constexpr int DMA_A = HALF / 1024 / 4;   // 8 one-KB DMA instructions per wave per operand
+  constexpr int DMA = 2 * DMA_A;           // 16 per wave per stage
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[2 * SLOT];
+
+  const int tiles_m = (int)((p.m + BM - 1) / BM);
+  const int tiles_n = (int)((p.n + BN - 1) / BN);
+  int tm, tn;
+  tile_coords(tiles_m, tiles_n, p.group_m, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave % WGM, wn = wave / WGM;
+
+  const int64_t rows_a = min((int64_t)BM, p.m - m0);
+  const int64_t rows_w = min((int64_t)BN, p.n - n0);
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + m0 * p.lda, (uint32_t)(rows_a * p.lda));
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w + n0 * p.ldw, (uint32_t)(rows_w * p.ldw));
+
+  // DMA lane map: 1 KB block b of an operand holds rows 8b..8b+7; lane l fills
+  // row 8b + l/8, slot l%8, from logical chunk (l%8) ^ lds_swizzle(row).  The
+  // swizzle depends on row % 16, i.e. on the parity of b, so two chunk values
+  // and two base offsets per operand cover all of a wave's blocks.
+  const int drow = lane >> 3;
+  const int dch0 = (lane & 7) ^ lds_swizzle(drow), dch1 = (lane & 7) ^ lds_swizzle(drow + 8);
+  const int row0 = wave * DMA_A * 8 + drow;
+  const uint32_t a_base0 = (uint32_t)(row0 * p.lda + dch0 * 16);
+  const uint32_t a_base1 = (uint32_t)((row0 + 8) * p.lda + dch1 * 16);
+  const uint32_t w_base0 = (uint32_t)(row0 * p.ldw + dch0 * 16);
+  const uint32_t w_base1 = (uint32_t)((row0 + 8) * p.ldw + dch1 * 16);
+  const uint32_t a_step = (uint32_t)(16 * p.lda), w_step = (uint32_t)(16 * p.ldw);
+  const int KT = (int)((p.k + BK - 1) / BK);
+  const uint32_t wave_lds = lds_addr(ring) + wave * DMA_A * 1024;
+
+  // DMA of stage s into slot j: instruction i < DMA_A is A block i, the rest W
+  // blocks; chunks past K (and whole stages past the end) read as zeros.
+  struct Dma {
+    uint32_t base, kb, kill0, kill1;
+  };
+  auto dma_setup = [&](int j, int s) {
+    const uint32_t kb = (uint32_t)s * BK;
+    return Dma{wave_lds + j * SLOT, kb, ((int64_t)kb + dch0 * 16 < p.k) ? 0u : VFA_OOB,
+               ((int64_t)kb + dch1 * 16 < p.k) ? 0u : VFA_OOB};
+  };
+  auto dma_one = [&](const Dma& d, auto i) {
+    if constexpr (i < DMA_A) {
+      const uint32_t off = (i % 2 ? a_base1 : a_base0) + (i / 2) * a_step + d.kb;
+      lds_dma16(ra, d.base + i * 1024, off | (i % 2 ? d.kill1 : d.kill0));
+    } else {
+      constexpr int w = i - DMA_A;
+      const uint32_t off = (w % 2 ? w_base1 : w_base0) + (w / 2) * w_step + d.kb;
+      lds_dma16(rw, d.base + HALF + w * 1024, off | (w % 2 ? d.kill1 : d.kill0));
+    }
+  };
+  auto issue = [&](int j, int s) {
+    const Dma d = dma_setup(j, s);
+    static_for<DMA>([&](auto i) { dma_one(d, i); });
+  };
+
+  const int fr = lane & 31, fh = lane >> 5;
+  const int fsw = lds_swizzle(fr);
+  v8i F[2][MB + NB];  // [K-substep][activation blocks, then weight blocks]
+  // Fragments of K-substep ks of the stage in slot j into register set ks.
+  auto read_one = [&](int j, auto ks, auto f) {
+    const int cc = ks * 4 + fh * 2;
+    const int o0 = (cc ^ fsw) << 4, o1 = ((cc + 1) ^ fsw) << 4;
+    const uint8_t* src = f < MB ? ring + j * SLOT + (wm * WM + fr) * BK + f * 32 * BK
+                                : ring + j * SLOT + HALF + (wn * WN + fr) * BK + (f - MB) * 32 * BK;
+    const v4i lo = *reinterpret_cast<const v4i*>(src + o0);
+    const v4i hi = *reinterpret_cast<const v4i*>(src + o1);
+    F[ks][f] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  };
+  auto read = [&](int j, auto ks) { static_for<MB + NB>([&](auto f) { read_one(j, ks, f); }); };
+  v16f acc[NB][MB];
+  static_for<NB>([&](auto i) { static_for<MB>([&](auto jj) { acc[i][jj] = v16f{}; }); });
+  // MFMAs number q0..q1-1 of K-substep ks (q = nb * MB + mb).
+  auto mfmas = [&](auto ks, auto q0, auto q1) {
+    static_for<q1 - q0>([&](auto qq) {
+      constexpr int q = q0 + qq, nb = q / MB, mb = q % MB;
+      acc[nb][mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+          F[ks][MB + nb], F[ks][mb], acc[nb][mb], 0, 0, 0, 0, 0, 0);
+    });
+  };
+  auto interleave = [&](auto n) {  // pair each of n MFMAs with one LDS read
+    static_for<n>([&](auto) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    });
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  constexpr int Q = MB * NB, QH = Q / 2;
+
+  issue(I0{}, 0);
+  issue(I1{}, 1);
+  wait_vmcnt<DMA, true>();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  read(I0{}, I0{});
+
+  // One stage per iteration; the slot index is a run-time value (unrolling
+  // two stages with constant slots raises register pressure past 256 VGPRs).
+  for (int kt = 0; kt < KT; ++kt) {
+    const int j = kt & 1;
+    // Substep 0 of stage kt, while reading substep 1 of the same stage.
+    mfmas(I0{}, I0{}, std::integral_constant<int, Q>{});
+    read(j, I1{});
+    interleave(std::integral_constant<int, 2 * (MB + NB)>{});
+    mfmas(I1{}, I0{}, std::integral_constant<int, QH>{});
+    // The MFMAs above stay above the wait (they keep the MFMA pipe busy while
+    // the wave waits); scheduling barriers pin the order.
+    __builtin_amdgcn_sched_barrier(0);
+    // Stage kt+1 has landed for every wave; stage kt is fully read.
+    wait_vmcnt<0, true>();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    // Second half: each remaining MFMA is followed by DMA / QH of the DMA
+    // instructions of stage kt+2 and by the reads of one fragment of stage kt+1
+    // (unused after the last stage), so DMA issue and reads overlap the MFMA pipe.
+    const Dma d = dma_setup(j, kt + 2);
+    static_for<QH>([&](auto i) {
+      constexpr int q = QH + i, nb = q / MB, mb = q % MB;
+      acc[nb][mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+          F[1][MB + nb], F[1][mb], acc[nb][mb], 0, 0, 0, 0, 0, 0);
+      static_for<DMA / QH>([&](auto t) { dma_one(d, std::integral_constant<int, i * (DMA / QH) + t>{}); });
+      if constexpr (i < MB + NB) read_one(1 - j, I0{}, i);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  }
+  wait_vmcnt<0, true>();  // every DMA has landed before the ring is reused
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  gemm_epilogue<BM, BN, WGM, WGN, EPI>(p, acc, m0, n0, wm, wn, (int)threadIdx.x, ring);
+}
+
+template <int EPI>
+static hipError_t launch_pipe2(const GemmParams& p, hipStream_t s) {
+  const int64_t tiles = ((p.m + 255) / 256) * ((p.n + 255) / 256);
+  fp8_gemm_pipe2<EPI><<<dim3((unsigned)tiles), dim3(256), 0, s>>>(p);
+  return hipGetLastError();
+}
+
 template <int WGM, int WGN, int EPI>
 static hipError_t launch_pipe(const GemmParams& p, hipStream_t s) {
   const int64_t tiles = ((p.m + 255) / 256) * ((p.n + 255) / 256);
@@ -462,10 +624,10 @@ static hipError_t launch_cfg(const GemmParams& p, hipStream_t s) {
 // whose row maxima need 64-column wave groups), 4 = 128x256 (2x2),
 // 5 = 256x128 (2x2), 6 = 256x256 (4x2: two waves per SIMD),
 // 7 = 256x256 (2x4: two waves per SIMD), 8 = 256x256 pipelined (2x2),
-// 9 = 256x256 pipelined (2x4).
+// 9 = 256x256 pipelined (2x4), 10 = 256x256 two-slot pipelined, 128-byte stages.
 int pick_tile(const GemmParams& p) {
   auto tiles = [&](int bm, int bn) { return ((p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn); };
-  if (tiles(256, 256) >= 512) return 6;
+  if (tiles(256, 256) >= 512) return 10;
   if (tiles(128, 128) >= 256) return 2;
   return 3;
 }
@@ -484,6 +646,7 @@ hipError_t launch_epi(const GemmParams& p, int tile, hipStream_t s) {
     case 7: return launch_cfg<256, 256, 2, 4, EPI>(p, s);
     case 8: return launch_pipe<2, 2, EPI>(p, s);
     case 9: return launch_pipe<2, 4, EPI>(p, s);
+    case 10: return launch_pipe2<EPI>(p, s);
     default: return hipErrorInvalidValue;
   }
 }
