@@ -168,8 +168,12 @@ int vflash_nvfp4_linear(const void* a, const float* sa, int64_t lda, const void*
 /*
  * Tuning hook: force a GEMM tile configuration for later calls in this process
  * (0 = automatic, 1 = 256x256, 2 = 128x128, 3 = 64x64, 4 = 128x256, 5 = 256x128,
- * 6 = 256x256 with 8 waves 4x2, 7 = 256x256 with 8 waves 2x4)
- * and the tile-order group height (0 = default).  Returns the previous tile value.
+ * 6 = 256x256 with 8 waves 4x2, 7 = 256x256 with 8 waves 2x4,
+ * 8 / 9 = 256x256 five-stage LDS-DMA ring with 4 / 8 waves,
+ * 10 = 256x256 two-slot 128-byte-stage LDS-DMA pipeline (default for large shapes),
+ * 11 = tile 10 as a persistent grid of one workgroup per CU)
+ * and the tile-order group height (0 = default).  Tiles other than 0..3 apply
+ * to the W8A8 GEMM family only.  Returns the previous tile value.
  */
 int vflash_set_gemm_tile(int tile, int group_m);
 

@@ -122,11 +122,13 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // LDS reads of other buffers may be scheduled around it; ordering against
 // reads of the destination comes from the caller's barrier, which is fenced
 // by "memory"-clobbering volatile statements that volatile DMAs never cross.
+// lds_dst must be wave-uniform in the compiler's analysis (derived from
+// scalars or readfirstlane), since it is passed in an SGPR.
 __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint32_t lds_dst,
                                           uint32_t voffset) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
-               : "s"(__builtin_amdgcn_readfirstlane(lds_dst)), "v"(voffset), "s"(r)
+               : "s"(lds_dst), "v"(voffset), "s"(r)
                : "m0");
 }
 

@@ -32,13 +32,8 @@ namespace vfa {
 // b % 8; renumbering gives each XCD a contiguous run of logical tiles, and a
 // grouped (GROUP_M tall) column sweep keeps the tiles that are resident on one
 // XCD at the same time sharing A rows and W rows in that XCD's L2.
-__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group_m, int& tm,
-                                            int& tn) {
-  const int nwg = gridDim.x;
-  const int b = blockIdx.x;
-  const int q = nwg >> 3, r = nwg & 7;
-  const int x = b & 7, i = b >> 3;
-  const int logical = x * q + min(x, r) + i;
+__device__ __forceinline__ void grouped_tile(int logical, int tiles_m, int tiles_n, int group_m,
+                                             int& tm, int& tn) {
   const int per_group = group_m * tiles_n;
   const int group = logical / per_group;
   const int first_m = group * group_m;
@@ -46,6 +41,15 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group_
   const int in_g = logical - group * per_group;
   tm = first_m + in_g % gs;
   tn = in_g / gs;
+}
+
+__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group_m, int& tm,
+                                            int& tn) {
+  const int nwg = gridDim.x;
+  const int b = blockIdx.x;
+  const int q = nwg >> 3, r = nwg & 7;
+  const int x = b & 7, i = b >> 3;
+  grouped_tile(x * q + min(x, r) + i, tiles_m, tiles_n, group_m, tm, tn);
 }
 
 // Epilogue shared by every tiling, in two phases through LDS.
@@ -343,7 +347,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) fp8_gemm_pipe(const GemmParams
   __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * 2 * HALF];
   static_assert(NS * 2 * HALF >= BM * BN * 2, "the ring doubles as the epilogue staging tile");
   auto slot = [&](auto j) -> uint8_t* { return ring + j * 2 * HALF; };
-  const uint32_t ring_lds = lds_addr(ring);
+  const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(ring));
 
   const int tiles_m = (int)((p.m + BM - 1) / BM);
   const int tiles_n = (int)((p.n + BN - 1) / BN);
@@ -372,7 +376,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) fp8_gemm_pipe(const GemmParams
 
   // DMA of stage s into ring slot j; chunks at or past K (including whole
   // stages past the end) are pointed beyond the buffer and arrive as zeros.
-  const uint32_t wave_lds = ring_lds + wave * DMA_A * 1024;
+  const uint32_t wave_lds = ring_lds + __builtin_amdgcn_readfirstlane(wave) * DMA_A * 1024;
   auto issue = [&](auto j, int s) {
     const uint32_t base = wave_lds + j * 2 * HALF;
     const int64_t kk = (int64_t)s * BK + dchunk * 16;
@@ -458,22 +462,27 @@ __global__ void __launch_bounds__(64 * WGM * WGN) fp8_gemm_pipe(const GemmParams
 //   8 MFMAs of substep 1, interleaved with the reads of stage kt+1 substep 0.
 // The DMA of a stage is issued about one stage of MFMA work before it is
 // needed; rows are stored with the lds_swizzle chunk permutation.
+constexpr int PIPE2_LDS = 2 * 2 * 256 * 128;  // two 64 KB stage slots
+
 template <int EPI>
-__global__ void __launch_bounds__(256) fp8_gemm_pipe2(const GemmParams p) {
+__device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, uint8_t* ring,
+                                           uint32_t ring_lds, int wave) {
   constexpr int BM = 256, BN = 256, BK = 128, WGM = 2, WGN = 2;
   constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
   constexpr int HALF = BM * BK;            // 32 KB: one operand of one stage
   constexpr int SLOT = 2 * HALF;           // 64 KB
   constexpr int DMA_A = HALF / 1024 / 4;   // 8 one-KB DMA instructions per wave per operand
   constexpr int DMA = 2 * DMA_A;           // 16 per wave per stage
-  __shared__ __attribute__((aligned(1024))) uint8_t ring[2 * SLOT];
+  static_assert(2 * SLOT == PIPE2_LDS, "slot layout");
 
-  const int tiles_m = (int)((p.m + BM - 1) / BM);
-  const int tiles_n = (int)((p.n + BN - 1) / BN);
-  int tm, tn;
-  tile_coords(tiles_m, tiles_n, p.group_m, tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // The lane index comes from mbcnt and the wave index arrives as a scalar, so
+  // in the persistent form no per-lane value stays live across tiles (holding
+  // the work-item id there costs a spill whose reload drains the stores).
+  int all = -1;
+  asm volatile("" : "+s"(all));  // opaque per tile: nothing below is hoisted out of a tile loop
+  const int lane = (int)__builtin_amdgcn_mbcnt_hi(all, __builtin_amdgcn_mbcnt_lo(all, 0));
+  const int tid_v = wave * 64 + lane;
   const int wm = wave % WGM, wn = wave / WGM;
 
   const int64_t rows_a = min((int64_t)BM, p.m - m0);
@@ -494,7 +503,7 @@ __global__ void __launch_bounds__(256) fp8_gemm_pipe2(const GemmParams p) {
   const uint32_t w_base1 = (uint32_t)((row0 + 8) * p.ldw + dch1 * 16);
   const uint32_t a_step = (uint32_t)(16 * p.lda), w_step = (uint32_t)(16 * p.ldw);
   const int KT = (int)((p.k + BK - 1) / BK);
-  const uint32_t wave_lds = lds_addr(ring) + wave * DMA_A * 1024;
+  const uint32_t wave_lds = ring_lds + wave * DMA_A * 1024;
 
   // DMA of stage s into slot j: instruction i < DMA_A is A block i, the rest W
   // blocks; chunks past K (and whole stages past the end) read as zeros.
@@ -595,13 +604,68 @@ __global__ void __launch_bounds__(256) fp8_gemm_pipe2(const GemmParams p) {
   wait_vmcnt<0, true>();  // every DMA has landed before the ring is reused
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  gemm_epilogue<BM, BN, WGM, WGN, EPI>(p, acc, m0, n0, wm, wn, (int)threadIdx.x, ring);
+  gemm_epilogue<BM, BN, WGM, WGN, EPI>(p, acc, m0, n0, wm, wn, tid_v, ring);
+}
+
+template <int EPI>
+__global__ void __launch_bounds__(256) fp8_gemm_pipe2(const GemmParams p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[PIPE2_LDS];
+  int tm, tn;
+  tile_coords((int)((p.m + 255) / 256), (int)((p.n + 255) / 256), p.group_m, tm, tn);
+  pipe2_tile<EPI>(p, tm, tn, ring, __builtin_amdgcn_readfirstlane(lds_addr(ring)),
+                  __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6));
+}
+
+// Persistent form: one workgroup per CU walks its share of the tiles, so the
+// epilogue stores of one tile drain while the next tile's first stages load.
+// Workgroup b runs on XCD b % 8; XCD x owns the x-th contiguous run of logical
+// tiles (grouped order), handed round-robin to the XCD's workgroups.
+template <int EPI>
+__global__ void __launch_bounds__(256) fp8_gemm_persist(const GemmParams p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[PIPE2_LDS];
+  const int tiles_m = (int)((p.m + 255) / 256), tiles_n = (int)((p.n + 255) / 256);
+  const int T = tiles_m * tiles_n, G = gridDim.x, b = blockIdx.x;
+  int first, end, stride;
+  if (G >= 8 && (G & 7) == 0) {
+    const int x = b & 7, q = T >> 3, rem = T & 7;
+    first = x * q + min(x, rem) + (b >> 3);
+    end = x * q + min(x, rem) + q + (x < rem ? 1 : 0);
+    stride = G >> 3;
+  } else {
+    first = b;
+    end = T;
+    stride = G;
+  }
+  // Scalars materialized once: the work-item id is dead afterwards.
+  int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(ring));
+  asm volatile("" : "+s"(wave), "+s"(ring_lds));
+  for (int logical = first; logical < end; logical += stride) {
+    int tm, tn;
+    grouped_tile(logical, tiles_m, tiles_n, p.group_m, tm, tn);
+    pipe2_tile<EPI>(p, tm, tn, ring, ring_lds, wave);
+    // Every wave has read its staged rows before the next tile's DMA reuses them.
+    wait_vmcnt<63, true>();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
 }
 
 template <int EPI>
 static hipError_t launch_pipe2(const GemmParams& p, hipStream_t s) {
   const int64_t tiles = ((p.m + 255) / 256) * ((p.n + 255) / 256);
   fp8_gemm_pipe2<EPI><<<dim3((unsigned)tiles), dim3(256), 0, s>>>(p);
+  return hipGetLastError();
+}
+
+int compute_units();
+
+template <int EPI>
+static hipError_t launch_persist(const GemmParams& p, hipStream_t s) {
+  const int64_t tiles = ((p.m + 255) / 256) * ((p.n + 255) / 256);
+  const int64_t grid = tiles < compute_units() ? tiles : compute_units();
+  fp8_gemm_persist<EPI><<<dim3((unsigned)grid), dim3(256), 0, s>>>(p);
   return hipGetLastError();
 }
 
@@ -624,7 +688,8 @@ static hipError_t launch_cfg(const GemmParams& p, hipStream_t s) {
 // whose row maxima need 64-column wave groups), 4 = 128x256 (2x2),
 // 5 = 256x128 (2x2), 6 = 256x256 (4x2: two waves per SIMD),
 // 7 = 256x256 (2x4: two waves per SIMD), 8 = 256x256 pipelined (2x2),
-// 9 = 256x256 pipelined (2x4), 10 = 256x256 two-slot pipelined, 128-byte stages.
+// 9 = 256x256 pipelined (2x4), 10 = 256x256 two-slot pipelined, 128-byte stages,
+// 11 = tile 10 as a persistent kernel (one workgroup per CU).
 int pick_tile(const GemmParams& p) {
   auto tiles = [&](int bm, int bn) { return ((p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn); };
   if (tiles(256, 256) >= 512) return 10;
@@ -647,8 +712,23 @@ hipError_t launch_epi(const GemmParams& p, int tile, hipStream_t s) {
     case 8: return launch_pipe<2, 2, EPI>(p, s);
     case 9: return launch_pipe<2, 4, EPI>(p, s);
     case 10: return launch_pipe2<EPI>(p, s);
+    case 11: return launch_persist<EPI>(p, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+// Compute units of the current device (cached per device id).
+int compute_units() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
 }
 
 hipError_t launch_fp8_gemm(const GemmParams& p, int epi, hipStream_t s) {
