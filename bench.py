@@ -12,7 +12,10 @@ events recorded on the launch stream around each of its launches in the timed
 region.  Prints one JSON line.
 
 Other workloads (``qkv``, ``ffn``, ``skinny``, ``nvfp4``, ``small``) print the
-same kind of line for the other shapes of this path.
+same kind of line for the other shapes of this path; ``copy`` times a plain
+1 GiB device copy, the calibration kernel for the HBM byte counters.  For the
+launch-bound shapes (``small``, ``skinny``) the line adds a device-side time
+per step measured with the launch queue filled ahead.
 """
 
 from __future__ import annotations
@@ -34,11 +37,15 @@ HBM_PEAK_GBS = 8000.0
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
     p.add_argument(
-        "--workload", default="fp8_linear", choices=["fp8_linear", "qkv", "ffn", "skinny", "nvfp4", "small"]
+        "--workload",
+        default="fp8_linear",
+        choices=["fp8_linear", "qkv", "ffn", "skinny", "nvfp4", "small", "copy"],
     )
+    p.add_argument("--skinny-m", type=int, default=1024)
+    p.add_argument("--skinny-n", type=int, default=6144)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--tile", type=int, default=0, help="force a GEMM tile configuration")
     p.add_argument("--group-m", type=int, default=0)
@@ -58,9 +65,11 @@ def seeded_linear(m, k, n, bias=True, seed=0):
     return x, codes, scale, b
 
 
-def traffic_from_profiles(kernel: str):
-    """HBM bytes per launch measured with rocprofv3 counters (committed summary)."""
-    path = ROOT / "profiles" / f"traffic_{kernel}.txt"
+def traffic_from_profiles(workload: str):
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3
+    summary of this workload (FETCH_SIZE and WRITE_SIZE scaled by the copy
+    calibration), or None when no counter run was summarised."""
+    path = ROOT / "profiles" / f"{workload}.txt"
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
@@ -103,7 +112,12 @@ def cpu_baseline_weight_only(x, codes, scale, b, flops_per_row):
 
 
 class EventTimer:
-    """HIP events on the launch stream around each launch of one kernel."""
+    """HIP events on the launch stream around each launch of one kernel.
+
+    The kernels run on torch's current stream (the C-ABI is handed
+    ``torch.cuda.current_stream()``), so events recorded on that stream bracket
+    exactly one launch each.
+    """
 
     def __init__(self):
         self.pairs = []
@@ -121,71 +135,99 @@ class EventTimer:
 
         self.pairs[-1][1].record(torch.cuda.current_stream())
 
-    def mean_ms(self):
-        return statistics.mean(s.elapsed_time(e) for s, e in self.pairs)
+    def times_ms(self):
+        return [s.elapsed_time(e) for s, e in self.pairs]
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(
-            "bench.py runs on one GPU: every box of this build has a single MI355X; "
-            "the multi-GPU sharding of this path is a design note, not a measured mode",
-            file=sys.stderr,
-        )
-        sys.exit(2)
+class Workload:
+    """One shape of the path: its step, the dominant kernel and its roofline units."""
+
+    def __init__(self, name, metric, unit, work, step, kernel, kernel_work, bound, peak, config,
+                 dtype="fp8_e4m3", cpu=None, launch_bound=False):
+        self.name = name
+        self.metric = metric  # metric string of the JSON line
+        self.unit = unit  # "TFLOP/s" or "GB/s"
+        self.work = work  # algorithmic FLOPs (or bytes) of one step
+        self.step = step  # step(i, timer or None)
+        self.kernel = kernel  # dominant kernel, named as in the rocprof summaries
+        self.kernel_work = kernel_work  # algorithmic FLOPs (or bytes) of one launch of it
+        self.bound = bound  # "mfma" or "hbm"
+        self.peak = peak
+        self.config = config
+        self.dtype = dtype
+        self.cpu = cpu
+        # Steps shorter than the host's launch cost: the GPU idles between
+        # launches, so device time is also measured with the queue filled ahead.
+        self.launch_bound = launch_bound
+
+
+def rate(work, ms, unit):
+    return work / (ms * 1e-3) / (1e12 if unit == "TFLOP/s" else 1e9)
+
+
+def linear_sets(m, k, n, count, dev):
+    """``count`` independent operand sets (seeds 0..count-1) resident in HBM.
+
+    Small shapes rotate over several sets so that the timed launches read HBM
+    rather than the 256 MB last-level cache.
+    """
+    sets = []
+    for seed in range(count):
+        x, codes, scale, b = seeded_linear(m, k, n, bias=True, seed=seed)
+        sets.append((x.to(dev), codes.to(dev), scale.to(dev), b.to(dev)))
+        if seed == 0:
+            host = (x, codes, scale, b)
+    return host, sets
+
+
+def make_workload(args, dev):
     import torch
 
-    from vflash_amd import _lib, kernels
+    from vflash_amd import kernels
     from vflash_amd.fp8_linear import RowFP8Execution
 
-    dev = torch.device("cuda:0")
-    if not _lib.is_gfx950(dev):
-        raise SystemExit("bench.py needs a gfx950 (MI355X) device")
-    _lib.library()
-    if args.tile or args.group_m:
-        _lib.set_gemm_tile(args.tile, args.group_m)
-
     wl = args.workload
-    timer = EventTimer()
-    cpu = None
     if wl in ("fp8_linear", "small", "qkv"):
         m, k, n = {"fp8_linear": (32760, 5120, 13824), "small": (4096, 3072, 3072),
                    "qkv": (32760, 5120, 15360)}[wl]
-        x, codes, scale, b = seeded_linear(m, k, n, bias=True)
-        xd, cd, sd, bd = x.to(dev), codes.to(dev), scale.to(dev), b.to(dev)
-        ex = RowFP8Execution("w8a8", activation_quantizer="triton")
+        host, sets = linear_sets(m, k, n, 8 if wl == "small" else 1, dev)
+        ex = RowFP8Execution("w8a8", activation_quantizer="hip")
+        # One call through the module API checks the drop-in path end to end; the
+        # timed step is the same pair of launches that RowFP8Execution.linear makes.
+        ex.linear(sets[0][0][:16], *sets[0][1:])
 
-        def step(timed):
+        def step(i, timer):
+            xd, cd, sd, bd = sets[i % len(sets)]
             a, sa = kernels.quantize_rows(xd)
-            if timed:
+            if timer:
                 timer.start()
             if wl == "qkv":
                 kernels.fp8_gemm_planes(a, sa, cd, sd, m, 3, bd)
             else:
                 kernels.fp8_gemm(a, sa, cd, sd, m, bd)
-            if timed:
+            if timer:
                 timer.stop()
 
-        # The timed step is the same pair of launches RowFP8Execution.linear makes;
-        # one call through the module API checks that path end to end first.
-        ex.linear(xd[:16], cd, sd, bd)
         flops = 2.0 * m * n * k
-        kernel = "fp8_gemm"
-        peak = FP8_PEAK_TFLOPS
-        config = {"workload": {"fp8_linear": "fp8_linear_ffn_up_shape", "small": "fp8_linear_small",
-                               "qkv": "merged_qkv_planes"}[wl],
-                  "m": m, "k": k, "n": n, "bias": True, "activation_quant": "per-token e4m3 (HIP)"}
-        if not args.no_cpu_baseline:
-            cpu = lambda: cpu_baseline_weight_only(x, codes, scale, b, 2.0 * n * k)
-    elif wl == "ffn":
+        names = {"fp8_linear": "fp8_linear_m32760_k5120_n13824", "small": "fp8_linear_m4096_k3072_n3072",
+                 "qkv": "merged_qkv_m32760_k5120_n15360_planes"}
+        metric = (f"FP8 linear TFLOP/s (M={m},K={k},N={n}) and % of gfx950 FP8 MFMA peak"
+                  if wl != "qkv" else "Merged QKV FP8 linear TFLOP/s (M=32760,K=5120,N=3x5120)")
+        config = {"workload": names[wl], "m": m, "k": k, "n": n, "bias": True,
+                  "activation_quant": "per-token e4m3 (HIP kernel)", "operand_sets": len(sets)}
+        if wl == "qkv":
+            config["output"] = "3 planes [32760, 40 heads, 128]"
+        cpu = None if args.no_cpu_baseline else (lambda: cpu_baseline_weight_only(*host, 2.0 * n * k))
+        return Workload(wl, metric, "TFLOP/s", flops, step, "fp8_gemm", flops, "mfma",
+                        FP8_PEAK_TFLOPS, config, cpu=cpu, launch_bound=wl == "small")
+
+    if wl == "ffn":
         from vflash_amd.fused import fp8_ffn
+        from vflash_amd.prepare import quantize_weight_rows
 
         m, h, f = 32760, 5120, 13824
         g = torch.Generator().manual_seed(0)
         x = torch.randn((m, h), generator=g).to(torch.bfloat16)
-        from vflash_amd.prepare import quantize_weight_rows
-
         wu = torch.randn((f, h), generator=g) * 0.02
         bu = (torch.randn(f, generator=g) * 0.01).to(torch.bfloat16)
         wdn = torch.randn((h, f), generator=g) * 0.02
@@ -195,57 +237,81 @@ def main():
         cu, su = quantize_weight_rows(wu)
         cdn, sdn = quantize_weight_rows(wdn)
         t = [v.to(dev) for v in (x, cu, su, bu, cdn, sdn, bdn, gate, res)]
-        ex = RowFP8Execution("w8a8", activation_quantizer="triton")
+        ex = RowFP8Execution("w8a8", activation_quantizer="hip")
+        fp8_ffn(ex, t[0][:64], t[1], t[2], t[3], t[4], t[5], t[6], t[7], t[8][:64])
 
-        def step(timed):
+        def step(i, timer):
             a, sa = kernels.quantize_rows(t[0])
-            if timed:
+            if timer:
                 timer.start()
             gg, amax = kernels.fp8_gemm_gelu(a, sa, t[1], t[2], m, t[3])
-            if timed:
+            if timer:
                 timer.stop()
             hc, hs = kernels.requant_rows(gg, amax)
             kernels.fp8_gemm_gate_residual(hc, hs, t[4], t[5], m, t[7], t[8], t[6])
 
-        fp8_ffn(ex, t[0][:64], t[1], t[2], t[3], t[4], t[5], t[6], t[7], t[8][:64])
-        flops = 4.0 * m * h * f
-        kernel = "fp8_gemm_gelu"
-        peak = FP8_PEAK_TFLOPS
-        config = {"workload": "fp8_ffn_gelu", "m": m, "hidden": h, "ffn": f}
+        cpu = None
         if not args.no_cpu_baseline:
             from oracle.baseline import gelu_ffn
 
             def cpu():
-                rows = 64
+                rows = 256
+                gelu_ffn(x[:32], cu, su, bu, cdn, sdn, bdn, gate, res[:32])  # warm-up
                 t0 = time.perf_counter()
                 gelu_ffn(x[:rows], cu, su, bu, cdn, sdn, bdn, gate, res[:rows])
                 dt = time.perf_counter() - t0
                 return {"value": 4.0 * h * f * rows / dt / 1e12, "unit": "TFLOP/s",
                         "cores": torch.get_num_threads(), "kind": "port",
-                        "sample": f"weight-only FFN chain on {rows} rows, one call"}
-    elif wl == "skinny":
+                        "sample": (f"weight-only FFN chain (dequantized bf16 weights, GELU-tanh, "
+                                   f"gate-residual) on {rows} of {m} rows, one call after a warm-up")}
+
+        return Workload(
+            wl, "Fused FP8 FFN TFLOP/s (M=32760, 5120 -> 13824 GELU-tanh -> 5120, gate-residual)",
+            "TFLOP/s", 4.0 * m * h * f, step, "fp8_gemm_gelu", 2.0 * m * h * f, "mfma", FP8_PEAK_TFLOPS,
+            {"workload": "fp8_ffn_m32760_h5120_f13824", "m": m, "hidden": h, "ffn": f,
+             "step": "quant, up GEMM + GELU + row amax, requant, down GEMM + gate-residual"},
+            cpu=cpu)
+
+    if wl == "skinny":
+        m, k, n, r = args.skinny_m, 1536, args.skinny_n, 32
+        per_set = m * k * 3 + n * k + 2 * m * n + 2 * r * (k + n) + 2 * m * r
+        count = max(2, int(600e6 // per_set) + 1)  # > 2x the last-level cache
+        sets = []
+        for seed in range(count):
+            x, codes, scale, b = seeded_linear(m, k, n, bias=True, seed=seed)
+            g = torch.Generator().manual_seed(1000 + seed)
+            la = (torch.randn((r, k), generator=g) * 0.01).to(torch.bfloat16)
+            lb = (torch.randn((n, r), generator=g) * 0.01).to(torch.bfloat16)
+            sets.append(tuple(v.to(dev) for v in (x, codes, scale, b, la, lb)))
         from vflash_amd.fused import fp8_linear_lora
 
-        m, k, n, r = 1024, 1536, 6144, 32
-        x, codes, scale, b = seeded_linear(m, k, n, bias=True)
-        g = torch.Generator().manual_seed(1)
-        la = (torch.randn((r, k), generator=g) * 0.01).to(torch.bfloat16)
-        lb = (torch.randn((n, r), generator=g) * 0.01).to(torch.bfloat16)
-        xd, cd, sd, bd, ad, bbd = (v.to(dev) for v in (x, codes, scale, b, la, lb))
-        ex = RowFP8Execution("w8a8", activation_quantizer="triton")
+        ex = RowFP8Execution("w8a8", activation_quantizer="hip")
+        fp8_linear_lora(ex, *sets[0])
 
-        def step(timed):
-            if timed:
+        def step(i, timer):
+            xd, cd, sd, bd, ad, bbd = sets[i % len(sets)]
+            a, sa = kernels.quantize_rows(xd)
+            tt = kernels.lora_down(xd, ad)
+            if timer:
                 timer.start()
-            fp8_linear_lora(ex, xd, cd, sd, bd, ad, bbd)
-            if timed:
+            kernels.fp8_gemm_lora(a, sa, cd, sd, m, tt, bbd, bias=bd)
+            if timer:
                 timer.stop()
 
-        flops = 2.0 * m * n * k + 2.0 * m * r * (k + n)
-        kernel = "fp8_linear_lora_call"
-        peak = FP8_PEAK_TFLOPS
-        config = {"workload": "skinny_lora", "m": m, "k": k, "n": n, "rank": r}
-    elif wl == "nvfp4":
+        # Algorithmic HBM bytes of the whole step: x read by the quant and LoRA-down
+        # kernels (bf16), codes written and read back (e4m3), row scales, weights
+        # (e4m3 + fp32 scale + bf16 bias), LoRA A and B, t written and read, bf16 out.
+        step_bytes = (2 * m * k * 2 + 2 * m * k + 8 * m + n * k + 6 * n
+                      + 2 * r * (k + n) + 4 * m * r + 2 * m * n)
+        gemm_bytes = m * k + 4 * m + n * k + 6 * n + 2 * m * r + 2 * n * r + 2 * m * n
+        return Workload(
+            wl, f"Skinny-M FP8 linear + rank-32 LoRA GB/s (M={m},K={k},N={n})", "GB/s", step_bytes, step,
+            "fp8_gemm_lora", gemm_bytes, "hbm", HBM_PEAK_GBS,
+            {"workload": f"skinny_lora_m{m}_k{k}_n{n}_r{r}", "m": m, "k": k, "n": n, "rank": r,
+             "operand_sets": count, "flops_per_step": 2.0 * m * n * k + 2.0 * m * r * (k + n)},
+            launch_bound=True)
+
+    if wl == "nvfp4":
         from vflash_amd.nvfp4_linear import NVFP4Execution, NVFP4Weight
         from vflash_amd.prepare import quantize_nvfp4_weight
 
@@ -256,37 +322,96 @@ def main():
         packed, scales, alpha, ins = quantize_nvfp4_weight(w)
         weight = NVFP4Weight(packed.to(dev), scales.to(dev), alpha.to(dev), ins.to(dev))
         xd = x.to(dev)
-        ex = NVFP4Execution()
+        NVFP4Execution().linear(xd[:16], weight)
 
-        def step(timed):
+        def step(i, timer):
             a, sa = kernels.quantize_rows(xd)
-            if timed:
+            if timer:
                 timer.start()
             kernels.nvfp4_gemm(a, sa, weight.packed, weight.scales, weight.alpha, m)
-            if timed:
+            if timer:
                 timer.stop()
 
-        ex.linear(xd[:16], weight)
         flops = 2.0 * m * n * k
-        kernel = "nvfp4_gemm"
-        peak = BF16_PEAK_TFLOPS
-        config = {"workload": "nvfp4_weight_linear", "m": m, "k": k, "n": n, "mfma": "bf16 (exact dequant)"}
+        return Workload(
+            wl, "NVFP4-weight linear TFLOP/s (M=32760,K=5120,N=13824)", "TFLOP/s", flops, step,
+            "nvfp4_gemm", flops, "mfma", BF16_PEAK_TFLOPS,
+            {"workload": "nvfp4_weight_linear_m32760_k5120_n13824", "m": m, "k": k, "n": n,
+             "mfma": "bf16 on exactly dequantized e2m1 x e4m3 weights"},
+            dtype="e4m3 activations x e2m1 weights (bf16 mfma)")
 
-    for _ in range(args.warmup):
-        step(False)
+    if wl == "copy":
+        # A plain device copy of 1 GiB: the calibration kernel for the HBM
+        # byte counters (FETCH_SIZE / WRITE_SIZE) of the rocprof summaries.
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+
+        def step(i, timer):
+            if timer:
+                timer.start()
+            dst.copy_(src)
+            if timer:
+                timer.stop()
+
+        nbytes = 2.0 * src.numel()
+        return Workload(wl, "HBM copy GB/s (1 GiB read + 1 GiB write)", "GB/s", nbytes, step, "copy",
+                        nbytes, "hbm", HBM_PEAK_GBS, {"workload": "hbm_copy_1GiB"}, dtype="u8")
+    raise ValueError(wl)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(
+            "bench.py runs on one GPU only: this path is measured on a single MI355X; "
+            "how it would shard over several GPUs is a design note, not a measured mode",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+    import torch
+
+    from vflash_amd import _lib
+
+    dev = torch.device("cuda:0")
+    if not _lib.is_gfx950(dev):
+        raise SystemExit("bench.py needs a gfx950 (MI355X) device")
+    _lib.library()
+    if args.tile or args.group_m:
+        _lib.set_gemm_tile(args.tile, args.group_m)
+
+    w = make_workload(args, dev)
+    timer = EventTimer()
+    for i in range(args.warmup):
+        w.step(i, None)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step(True)
+    for i in range(args.steps):
+        w.step(i, timer)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1e3 / args.steps
-    kernel_ms = timer.mean_ms()
-    kernel_tflops = flops / (kernel_ms * 1e-3) / 1e12
+    times = timer.times_ms()
+    device = None
+    if w.launch_bound:
+        # Hold the stream with a spin kernel while the host enqueues every step,
+        # then time the same steps on the device with events around the run.
+        timer = EventTimer()
+        torch.cuda._sleep(100_000_000)
+        first = torch.cuda.Event(enable_timing=True)
+        last = torch.cuda.Event(enable_timing=True)
+        first.record(torch.cuda.current_stream())
+        for i in range(args.steps):
+            w.step(i, timer)
+        last.record(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        times = timer.times_ms()
+        device = first.elapsed_time(last) / args.steps
+    kernel_ms = statistics.mean(times)
+    achieved = rate(w.kernel_work, kernel_ms, w.unit)
     line = {
-        "metric": "FP8 linear TFLOP/s (M=32760,K=5120,N=13824) and % of gfx950 FP8 MFMA peak",
-        "value": flops / (ms_per_step * 1e-3) / 1e12,
-        "unit": "TFLOP/s",
+        "metric": w.metric,
+        "value": rate(w.work, ms_per_step, w.unit),
+        "unit": w.unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -294,22 +419,28 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8_e4m3" if wl != "nvfp4" else "fp8_e4m3 x e2m1 (bf16 mfma)",
-        "data": "synthetic (seed 0, BASELINE recipe)",
-        "config": config,
+        "dtype": w.dtype,
+        "data": "synthetic: seeded N(0,1) activations, N(0,0.02) weights quantized per row, N(0,0.01) bias",
+        "config": w.config,
         "roofline": {
-            "bound": "mfma",
-            "achieved": kernel_tflops,
-            "peak": peak,
-            "unit": "TFLOP/s",
-            "frac": kernel_tflops / peak,
-            "traffic": traffic_from_profiles(kernel if wl != "ffn" else "fp8_gemm_gelu"),
-            "kernel": kernel,
-            "kernel_ms": kernel_ms,
+            "bound": w.bound,
+            "achieved": achieved,
+            "peak": w.peak,
+            "unit": w.unit,
+            "frac": achieved / w.peak,
+            "traffic": traffic_from_profiles(w.config["workload"]),
+            "kernel": w.kernel,
+            "kernel_ms_mean": kernel_ms,
+            "kernel_ms_median": statistics.median(times),
+            "launches_timed": len(times),
         },
-        "cpu_baseline": cpu() if cpu is not None else None,
+        "cpu_baseline": w.cpu() if w.cpu is not None else None,
     }
-    print(json.dumps(line))
+    if device is not None:
+        line["device_ms_per_step"] = device
+        line["device_rate"] = rate(w.work, device, w.unit)
+        line["roofline"]["timing"] = "device queue filled ahead of the launches"
+    print(json.dumps(line), flush=True)
 
 
 if __name__ == "__main__":
