@@ -337,8 +337,8 @@ def make_workload(args, dev):
             wl, "NVFP4-weight linear TFLOP/s (M=32760,K=5120,N=13824)", "TFLOP/s", flops, step,
             "nvfp4_gemm", flops, "mfma", BF16_PEAK_TFLOPS,
             {"workload": "nvfp4_weight_linear_m32760_k5120_n13824", "m": m, "k": k, "n": n,
-             "mfma": "bf16 on exactly dequantized e2m1 x e4m3 weights"},
-            dtype="e4m3 activations x e2m1 weights (bf16 mfma)")
+             "mfma": "f16 on exactly dequantized e4m3 activations and e2m1 x e4m3 weights"},
+            dtype="e4m3 activations x e2m1 weights (f16 mfma, exact operands)")
 
     if wl == "copy":
         # A plain device copy of 1 GiB: the calibration kernel for the HBM

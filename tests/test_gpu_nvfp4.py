@@ -35,8 +35,8 @@ def tile():
     _lib.set_gemm_tile(0)
 
 
-@pytest.mark.parametrize("cfg", [1, 2, 3])
-@pytest.mark.parametrize("m,n,k", [(1, 128, 64), (37, 256, 192), (300, 384, 512)])
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4])
+@pytest.mark.parametrize("m,n,k", [(1, 128, 64), (37, 256, 192), (300, 384, 512), (513, 640, 1088)])
 def test_small_shapes_every_tile(dev, tile, cfg, m, n, k):
     _lib.set_gemm_tile(cfg)
     x, (packed, scales, alpha, ins), b = make(m, n, k, seed=m + n + k)

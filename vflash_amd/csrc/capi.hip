@@ -54,6 +54,7 @@ vfa::GemmParams base_params(const void* a, const float* sa, int64_t lda, const v
   p.sa = sa;
   p.w = static_cast<const uint8_t*>(w);
   p.sw = sw;
+  p.sw_step = 1;
   p.lda = lda;
   p.ldw = ldw;
   p.m = m;
@@ -212,7 +213,10 @@ int vflash_nvfp4_linear(const void* a, const float* sa, int64_t lda, const void*
   if (bias && !aligned(bias, 2)) return VFLASH_EINVAL;
   if (!aligned(alpha, 4)) return VFLASH_EINVAL;
   if (256 * lda >= (int64_t(1) << 31)) return VFLASH_EINVAL;
-  const int tile = (g_tile >= 1 && g_tile <= 3) ? g_tile : 0;
+  int tile = (g_tile >= 1 && g_tile <= 4) ? g_tile : 0;
+  // The pipelined kernel copies block scales with 16-byte DMA; other alignments
+  // use the register-staged kernels.
+  if (!aligned(w_scales, 16) && (tile == 0 || tile == 4)) tile = 2;
   return status(vfa::launch_nvfp4(static_cast<const uint8_t*>(a), sa, lda,
                                   static_cast<const uint8_t*>(w_packed),
                                   static_cast<const uint8_t*>(w_scales), alpha, m, n, k,

@@ -10,7 +10,9 @@ struct GemmParams {
   const uint8_t* a;  // activation codes [m, k], row stride lda bytes
   const float* sa;   // per-row activation scales [m]
   const uint8_t* w;  // weight codes [n, k], row stride ldw bytes
-  const float* sw;   // per-output-channel weight scales [n]
+  const float* sw;   // weight scales: sw[n * sw_step] (sw_step 0: one scalar)
+  int64_t sw_step;
+  const uint8_t* wsb;  // E2M1-weight GEMM: E4M3 block scales in the 128x4 order
   int64_t lda, ldw, m, n, k;
   const uint16_t* bias;  // bf16 [n] or null
   uint16_t* out;         // bf16, row stride ldo elements

@@ -8,14 +8,16 @@
 // per-token E4M3 code of the W8A8 path instead of an NVFP4 activation.
 //
 // Every product e2m1 * e4m3 has at most 6 significant bits, so it is exact in
-// bfloat16, and every E4M3 code is exact in bfloat16: the contraction runs on
-// v_mfma_f32_32x32x16_bf16 with no rounding before the binary32 accumulator.
-// Weights stay packed (0.5 byte/element) in HBM and are dequantized while
-// being staged into LDS, once per workgroup tile, so the four waves read ready
-// bf16 fragments.  Scales use the 128x4 tiled order of NVFP4Weight
+// bfloat16 and in binary16, and so is every E4M3 code: the contraction has no
+// rounding ahead of the binary32 accumulator.  Two kernels:
+//   nvfp4_gemm_pipe (large shapes): packed operands staged in LDS by DMA and
+//     dequantized in registers into f16 MFMA operands;
+//   nvfp4_gemm_kernel (small shapes): weights dequantized to bf16 while being
+//     staged into LDS, once per workgroup tile, feeding bf16 MFMAs.
+// Weights stay packed (0.5 byte/element) in HBM.  Scales use the 128x4 tiled order of NVFP4Weight
 // (h3_nvfp4_linear.py:22-33): for row n and K block j (16 elements),
 //   off = (n/128)*(K/64)*512 + (j/4)*512 + (n%32)*16 + ((n%128)/32)*4 + j%4.
-#include "common.h"
+#include "gemm_epilogue.h"
 
 namespace vfa {
 
@@ -42,22 +44,6 @@ __device__ __forceinline__ uint32_t pack_exact_bf16(float lo, float hi) {
   return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
 }
 
-__device__ __forceinline__ void tile_coords_fp4(int tiles_m, int tiles_n, int group_m, int& tm,
-                                                int& tn) {
-  const int nwg = gridDim.x;
-  const int b = blockIdx.x;
-  const int q = nwg >> 3, r = nwg & 7;
-  const int x = b & 7, i = b >> 3;
-  const int logical = x * q + min(x, r) + i;
-  const int per_group = group_m * tiles_n;
-  const int group = logical / per_group;
-  const int first_m = group * group_m;
-  const int gs = min(tiles_m - first_m, group_m);
-  const int in_g = logical - group * per_group;
-  tm = first_m + in_g % gs;
-  tn = in_g / gs;
-}
-
 template <int BM, int BN>
 __global__ void __launch_bounds__(256) nvfp4_gemm_kernel(const Fp4Params p) {
   constexpr int BK = 64;              // K elements per stage; 128 bytes of bf16 per LDS row
@@ -71,7 +57,7 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_kernel(const Fp4Params p) {
 
   const int tiles_m = (int)((p.m + BM - 1) / BM), tiles_n = (int)((p.n + BN - 1) / BN);
   int tm, tn;
-  tile_coords_fp4(tiles_m, tiles_n, p.group_m, tm, tn);
+  tile_coords(tiles_m, tiles_n, p.group_m, tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -217,6 +203,188 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_kernel(const Fp4Params p) {
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Pipelined 256x256 W4A8 kernel: packed operands in LDS, dequantization in
+// registers, f16 MFMA.
+//
+// Every E4M3 code and every product e2m1 * e4m3 (at most 6 significant bits,
+// magnitude 2^-10 .. 2688) is exact in binary16, so the contraction runs on
+// v_mfma_f32_32x32x16_f16 with no rounding ahead of the binary32 accumulator,
+// the same sum as the bf16 form.  binary16 is used because its packed multiply
+// (v_pk_mul_f16) applies the E4M3 block scale exactly in one instruction; the
+// hardware-scaled converters take only the exponent of their scale operand.
+//
+// LDS holds each stage (128 K) as it sits in HBM: A codes (256 rows x 128 B),
+// packed weights (256 rows x 64 B) and the stage's block scales (two 1 KB
+// runs of the 128x4 order), filled by buffer-load-to-LDS DMA, two slots.  A
+// lane dequantizes only the values it feeds to its MFMAs:
+//   A: v_cvt_scalef32_pk_f16_fp8 (scale 1), two codes per instruction;
+//   W: v_cvt_scalef32_pk_f16_fp4 (scale 1) then v_pk_mul_f16 by the block
+//      scale, two values per two instructions.
+// K is consumed in a lane-friendly order (the sum does not depend on it): for
+// MFMA step v of a 64-K half u, lanes 0-31 supply K 64u + 8v .. +7 and lanes
+// 32-63 supply K 64u + 32 + 8v .. +7, so each lane reads 32 contiguous codes
+// and 16 contiguous packed bytes (one or two 16-element scale blocks) per half.
+constexpr int FP4_A = 256 * 128;
+constexpr int FP4_W = 256 * 64;
+constexpr int FP4_S = 2 * 1024;
+constexpr int FP4_SLOT = FP4_A + FP4_W + FP4_S;
+constexpr int FP4_LDS = 256 * 256 * 2;  // also the epilogue's bf16 staging tile
+static_assert(2 * FP4_SLOT <= FP4_LDS, "ring fits the staging buffer");
+
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+__global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[FP4_LDS];
+  constexpr int MB = 4, NB = 4;
+  const int tiles_m = (int)((p.m + 255) / 256), tiles_n = (int)((p.n + 255) / 256);
+  int tm, tn;
+  tile_coords(tiles_m, tiles_n, p.group_m, tm, tn);
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = (int)threadIdx.x & 63;
+  const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(ring));
+  const int wm = wave & 1, wn = wave >> 1;
+  const int64_t m0 = (int64_t)tm * 256, n0 = (int64_t)tn * 256;
+  const int64_t k_tiles = p.k / 64;  // 128x4 scale tiles along K
+  const int64_t rows_a = min((int64_t)256, p.m - m0);
+  const int64_t rows_w = min((int64_t)256, p.n - n0);  // 128 or 256 (n % 128 == 0)
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + m0 * p.lda, (uint32_t)(rows_a * p.lda));
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w + n0 * p.ldw, (uint32_t)(rows_w * p.ldw));
+  const __amdgpu_buffer_rsrc_t rs =
+      make_rsrc(p.wsb + (n0 / 128) * k_tiles * 512, (uint32_t)((rows_w / 128) * k_tiles * 512));
+
+  // DMA lane maps.  A: 1 KB block i of a wave = rows wave*64 + 8i .. +7, lane l
+  // fills row + l/8, slot l%8 with logical chunk (l%8) ^ lds_swizzle(row).
+  const int drow = lane >> 3;
+  const int ach0 = (lane & 7) ^ lds_swizzle(drow), ach1 = (lane & 7) ^ lds_swizzle(drow + 8);
+  const uint32_t a_base0 = (uint32_t)((wave * 64 + drow) * p.lda + ach0 * 16);
+  const uint32_t a_base1 = (uint32_t)((wave * 64 + drow + 8) * p.lda + ach1 * 16);
+  const uint32_t a_step = (uint32_t)(16 * p.lda);
+  // W: 64-byte rows; 1 KB block i of a wave = rows wave*64 + 16i .. +15, lane
+  // l fills row + l/4, slot l%4 with logical chunk (l%4) ^ ((row >> 2) & 3).
+  const int wch = (lane & 3) ^ ((lane >> 4) & 3);
+  const uint32_t w_base = (uint32_t)((wave * 64 + (lane >> 2)) * p.ldw + wch * 16);
+  const uint32_t w_step = (uint32_t)(16 * p.ldw);
+  // Scales: waves 0 and 1 copy the stage's 1 KB (K tiles 2s, 2s+1) of row tile `wave`.
+  const uint32_t s_base = (uint32_t)(wave * k_tiles * 512 + lane * 16);
+  const uint32_t dst_a = ring_lds + wave * 8192, dst_w = ring_lds + FP4_A + wave * 4096;
+  const uint32_t dst_s = ring_lds + FP4_A + FP4_W + wave * 1024;
+  const int KT = (int)((p.k + 127) / 128);
+
+  auto issue = [&](int j, int s) {
+    const uint32_t slot = (uint32_t)j * FP4_SLOT;
+    const int64_t kb = (int64_t)s * 128;
+    const uint32_t kill0 = kb + ach0 * 16 < p.k ? 0u : VFA_OOB;
+    const uint32_t kill1 = kb + ach1 * 16 < p.k ? 0u : VFA_OOB;
+    static_for<8>([&](auto i) {
+      const uint32_t off = (i % 2 ? a_base1 : a_base0) + (i / 2) * a_step + (uint32_t)kb;
+      lds_dma16(ra, dst_a + slot + i * 1024, off | (i % 2 ? kill1 : kill0));
+    });
+    const int64_t kw = kb / 2;
+    const uint32_t killw = kw + wch * 16 < p.ldw ? 0u : VFA_OOB;
+    static_for<4>([&](auto i) {
+      lds_dma16(rw, dst_w + slot + i * 1024, (w_base + i * w_step + (uint32_t)kw) | killw);
+    });
+    if (wave < 2) {
+      const uint32_t kills = 2 * (int64_t)s + (lane >> 5) < k_tiles ? 0u : VFA_OOB;
+      lds_dma16(rs, dst_s + slot, (s_base + (uint32_t)s * 1024) | kills);
+    }
+  };
+
+  const int fr = lane & 31, fh = lane >> 5;
+  const int asw = lds_swizzle(fr), wsw = (fr >> 2) & 3;
+  struct Raw {
+    v4i a[MB][2];
+    v4i w[NB];
+    uint32_t s[NB];
+  };
+  // The packed operands of 64-K half u of the stage in slot j.
+  auto read_raw = [&](Raw& r, int j, auto u) {
+    const uint8_t* base = ring + j * FP4_SLOT;
+    static_for<MB>([&](auto mb) {
+      const uint8_t* row = base + (wm * 128 + mb * 32 + fr) * 128;
+      r.a[mb][0] = *reinterpret_cast<const v4i*>(row + (((4 * u + 2 * fh) ^ asw) << 4));
+      r.a[mb][1] = *reinterpret_cast<const v4i*>(row + (((4 * u + 2 * fh + 1) ^ asw) << 4));
+    });
+    static_for<NB>([&](auto nb) {
+      const uint8_t* row = base + FP4_A + (wn * 128 + nb * 32 + fr) * 64;
+      r.w[nb] = *reinterpret_cast<const v4i*>(row + (((2 * u + fh) ^ wsw) << 4));
+      r.s[nb] = *reinterpret_cast<const uint32_t*>(base + FP4_A + FP4_W + wn * 1024 + u * 512 +
+                                                   fr * 16 + nb * 4);
+    });
+  };
+
+  v16f acc[NB][MB];
+  static_for<NB>([&](auto i) { static_for<MB>([&](auto jj) { acc[i][jj] = v16f{}; }); });
+  // MFMA step v (0..3) of a half held in r.
+  auto step = [&](const Raw& r, auto v) {
+    v8h xa[MB], xw[NB];
+    static_for<MB>([&](auto mb) {
+      const uint32_t d0 = (uint32_t)r.a[mb][v / 2][(v % 2) * 2];
+      const uint32_t d1 = (uint32_t)r.a[mb][v / 2][(v % 2) * 2 + 1];
+      const v2h x0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, false);
+      const v2h x1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, true);
+      const v2h x2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, false);
+      const v2h x3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, true);
+      xa[mb] = v8h{x0[0], x0[1], x1[0], x1[1], x2[0], x2[1], x3[0], x3[1]};
+    });
+    static_for<NB>([&](auto nb) {
+      // Block scale of this lane's 8 values: byte 2*fh + v/2 of the row's word.
+      const uint32_t sb = (r.s[nb] >> (16 * fh + 8 * (v / 2))) & 0xffu;
+      const v2h sc = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(sb | (sb << 8), 1.0f, false);
+      const uint32_t d = (uint32_t)r.w[nb][(int)v];
+      const v2h y0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.0f, 0) * sc;
+      const v2h y1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.0f, 1) * sc;
+      const v2h y2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.0f, 2) * sc;
+      const v2h y3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.0f, 3) * sc;
+      xw[nb] = v8h{y0[0], y0[1], y1[0], y1[1], y2[0], y2[1], y3[0], y3[1]};
+    });
+    static_for<NB>([&](auto nb) {
+      static_for<MB>([&](auto mb) {
+        acc[nb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xw[nb], xa[mb], acc[nb][mb], 0, 0, 0);
+      });
+    });
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+
+  Raw r0, r1;
+  issue(0, 0);
+  issue(1, 1);
+  wait_vmcnt<0, true>();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  read_raw(r0, 0, I0{});
+  for (int kt = 0; kt < KT; ++kt) {
+    const int j = kt & 1;
+    read_raw(r1, j, I1{});
+    step(r0, I0{});
+    step(r0, I1{});
+    step(r0, I2{});
+    step(r0, I3{});
+    step(r1, I0{});
+    step(r1, I1{});
+    __builtin_amdgcn_sched_barrier(0);
+    // Stage kt+1 has landed for every wave and stage kt is fully read.
+    wait_vmcnt<0, true>();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue(j, kt + 2);
+    read_raw(r0, 1 - j, I0{});
+    step(r1, I2{});
+    step(r1, I3{});
+  }
+  wait_vmcnt<0, true>();  // every DMA has landed before the ring becomes the staging tile
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  gemm_epilogue<256, 256, 2, 2, EPI_BIAS>(p, acc, m0, n0, wm, wn, (int)threadIdx.x, ring);
+}
+
 hipError_t launch_nvfp4_gemm(const Fp4Params& p, int tile, hipStream_t s) {
   auto go = [&](auto bm, auto bn) {
     constexpr int BM = decltype(bm)::value, BN = decltype(bn)::value;
@@ -230,7 +398,28 @@ hipError_t launch_nvfp4_gemm(const Fp4Params& p, int tile, hipStream_t s) {
   if (tile == 0) {
     const int64_t big = ((p.m + 255) / 256) * ((p.n + 255) / 256);
     const int64_t mid = ((p.m + 127) / 128) * ((p.n + 127) / 128);
-    tile = big >= 512 ? 1 : (mid >= 256 ? 2 : 3);
+    tile = big >= 256 ? 4 : (mid >= 256 ? 2 : 3);
+  }
+  if (tile == 4) {
+    GemmParams g{};
+    g.a = p.a;
+    g.sa = p.sa;
+    g.lda = p.lda;
+    g.w = p.w;
+    g.ldw = p.k / 2;
+    g.wsb = p.ws;
+    g.sw = p.alpha;
+    g.sw_step = 0;
+    g.m = p.m;
+    g.n = p.n;
+    g.k = p.k;
+    g.bias = p.bias;
+    g.out = p.out;
+    g.ldo = p.ldo;
+    g.group_m = p.group_m;
+    const int64_t tiles = ((p.m + 255) / 256) * ((p.n + 255) / 256);
+    nvfp4_gemm_pipe<<<dim3((unsigned)tiles), dim3(256), 0, s>>>(g);
+    return hipGetLastError();
   }
   switch (tile) {
     case 1: return go(I256{}, I256{});
