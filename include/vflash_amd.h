@@ -171,7 +171,8 @@ int vflash_nvfp4_linear(const void* a, const float* sa, int64_t lda, const void*
  * 6 = 256x256 with 8 waves 4x2, 7 = 256x256 with 8 waves 2x4,
  * 8 / 9 = 256x256 five-stage LDS-DMA ring with 4 / 8 waves,
  * 10 = 256x256 two-slot 128-byte-stage LDS-DMA pipeline (default for large shapes),
- * 11 = tile 10 as a persistent grid of one workgroup per CU)
+ * 11 = tile 10 as a persistent grid of one workgroup per CU,
+ * 12 = 128x128 two-slot pipeline, two workgroups per CU)
  * and the tile-order group height (0 = default).  For vflash_nvfp4_linear the
  * values mean 1 = 256x256, 2 = 128x128, 3 = 64x128 (register-staged) and
  * 4 = 256x256 pipelined (default for large shapes); other values select the

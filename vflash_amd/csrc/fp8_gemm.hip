@@ -290,18 +290,22 @@ __global__ void __launch_bounds__(64 * WGM * WGN) fp8_gemm_pipe(const GemmParams
 //   8 MFMAs of substep 1, interleaved with the reads of stage kt+1 substep 0.
 // The DMA of a stage is issued about one stage of MFMA work before it is
 // needed; rows are stored with the lds_swizzle chunk permutation.
-constexpr int PIPE2_LDS = 2 * 2 * 256 * 128;  // two 64 KB stage slots
+// Ring bytes of the two-slot pipeline for a BT x BT tile (BT = 256 or 128).
+constexpr int pipe2_lds(int bt) { return 2 * 2 * bt * 128; }
+constexpr int PIPE2_LDS = pipe2_lds(256);  // two 64 KB stage slots
 
-template <int EPI>
+template <int EPI, int BT = 256>
 __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, uint8_t* ring,
-                                           uint32_t ring_lds, int wave) {
-  constexpr int BM = 256, BN = 256, BK = 128, WGM = 2, WGN = 2;
+                                           uint32_t ring_lds, uint8_t* vec, uint32_t vec_lds,
+                                           int wave) {
+  constexpr int BM = BT, BN = BT, BK = 128, WGM = 2, WGN = 2;
   constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
-  constexpr int HALF = BM * BK;            // 32 KB: one operand of one stage
-  constexpr int SLOT = 2 * HALF;           // 64 KB
-  constexpr int DMA_A = HALF / 1024 / 4;   // 8 one-KB DMA instructions per wave per operand
-  constexpr int DMA = 2 * DMA_A;           // 16 per wave per stage
-  static_assert(2 * SLOT == PIPE2_LDS, "slot layout");
+  constexpr int HALF = BM * BK;            // one operand of one stage (32 KB at BT = 256)
+  constexpr int SLOT = 2 * HALF;
+  constexpr int DMA_A = HALF / 1024 / 4;   // one-KB DMA instructions per wave per operand
+  constexpr int DMA = 2 * DMA_A;           // per wave per stage
+  static_assert(2 * SLOT == pipe2_lds(BT), "slot layout");
+  static_assert(DMA_A % 2 == 0, "A blocks alternate between the two swizzle parities");
 
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   // The lane index comes from mbcnt and the wave index arrives as a scalar, so
@@ -391,7 +395,10 @@ __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, 
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   constexpr int Q = MB * NB, QH = Q / 2;
+  constexpr int RD = 2 * (MB + NB);  // ds_read_b128 per K-substep
+  static_assert(DMA % QH == 0, "DMA instructions spread evenly over the second half");
 
+  stage_vectors<BM, BN>(p, m0, n0, wave, lane, vec_lds);
   issue(I0{}, 0);
   issue(I1{}, 1);
   wait_vmcnt<DMA, true>();
@@ -406,7 +413,7 @@ __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, 
     // Substep 0 of stage kt, while reading substep 1 of the same stage.
     mfmas(I0{}, I0{}, std::integral_constant<int, Q>{});
     read(j, I1{});
-    interleave(std::integral_constant<int, 2 * (MB + NB)>{});
+    interleave(std::integral_constant<int, (RD < Q ? RD : Q)>{});
     mfmas(I1{}, I0{}, std::integral_constant<int, QH>{});
     // The MFMAs above stay above the wait (they keep the MFMA pipe busy while
     // the wave waits); scheduling barriers pin the order.
@@ -428,20 +435,40 @@ __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, 
       if constexpr (i < MB + NB) read_one(1 - j, I0{}, i);
       __builtin_amdgcn_sched_barrier(0);
     });
+    // Fragments not covered above (smaller tiles have fewer MFMAs than fragments).
+    static_for<(MB + NB > QH ? MB + NB - QH : 0)>([&](auto i) {
+      read_one(1 - j, I0{}, std::integral_constant<int, QH + i>{});
+    });
   }
   wait_vmcnt<0, true>();  // every DMA has landed before the ring is reused
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  gemm_epilogue<BM, BN, WGM, WGN, EPI>(p, acc, m0, n0, wm, wn, tid_v, ring);
+  gemm_epilogue<BM, BN, WGM, WGN, EPI, true>(p, acc, m0, n0, wm, wn, tid_v, ring, vec);
 }
 
 template <int EPI>
 __global__ void __launch_bounds__(256) fp8_gemm_pipe2(const GemmParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t ring[PIPE2_LDS];
+  __shared__ __attribute__((aligned(1024))) uint8_t vec[VEC_LDS];
   int tm, tn;
   tile_coords((int)((p.m + 255) / 256), (int)((p.n + 255) / 256), p.group_m, tm, tn);
-  pipe2_tile<EPI>(p, tm, tn, ring, __builtin_amdgcn_readfirstlane(lds_addr(ring)),
+  pipe2_tile<EPI>(p, tm, tn, ring, __builtin_amdgcn_readfirstlane(lds_addr(ring)), vec,
+                  __builtin_amdgcn_readfirstlane(lds_addr(vec)),
                   __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6));
+}
+
+// 128 x 128 form for shapes with too few 256 x 256 tiles to fill the GPU: the
+// same pipeline with 64 x 64 per wave (64 accumulator registers), so that two
+// workgroups share a CU and each hides the other's DMA latency and epilogue.
+template <int EPI>
+__global__ void __launch_bounds__(256, 2) fp8_gemm_pipe2s(const GemmParams p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[pipe2_lds(128)];
+  __shared__ __attribute__((aligned(1024))) uint8_t vec[VEC_LDS];
+  int tm, tn;
+  tile_coords((int)((p.m + 127) / 128), (int)((p.n + 127) / 128), p.group_m, tm, tn);
+  pipe2_tile<EPI, 128>(p, tm, tn, ring, __builtin_amdgcn_readfirstlane(lds_addr(ring)), vec,
+                       __builtin_amdgcn_readfirstlane(lds_addr(vec)),
+                       __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6));
 }
 
 // Persistent form: one workgroup per CU walks its share of the tiles, so the
@@ -451,6 +478,7 @@ __global__ void __launch_bounds__(256) fp8_gemm_pipe2(const GemmParams p) {
 template <int EPI>
 __global__ void __launch_bounds__(256) fp8_gemm_persist(const GemmParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t ring[PIPE2_LDS];
+  __shared__ __attribute__((aligned(1024))) uint8_t vec[VEC_LDS];
   const int tiles_m = (int)((p.m + 255) / 256), tiles_n = (int)((p.n + 255) / 256);
   const int T = tiles_m * tiles_n, G = gridDim.x, b = blockIdx.x;
   int first, end, stride;
@@ -467,11 +495,12 @@ __global__ void __launch_bounds__(256) fp8_gemm_persist(const GemmParams p) {
   // Scalars materialized once: the work-item id is dead afterwards.
   int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(ring));
-  asm volatile("" : "+s"(wave), "+s"(ring_lds));
+  uint32_t vec_lds = __builtin_amdgcn_readfirstlane(lds_addr(vec));
+  asm volatile("" : "+s"(wave), "+s"(ring_lds), "+s"(vec_lds));
   for (int logical = first; logical < end; logical += stride) {
     int tm, tn;
     grouped_tile(logical, tiles_m, tiles_n, p.group_m, tm, tn);
-    pipe2_tile<EPI>(p, tm, tn, ring, ring_lds, wave);
+    pipe2_tile<EPI>(p, tm, tn, ring, ring_lds, vec, vec_lds, wave);
     // Every wave has read its staged rows before the next tile's DMA reuses them.
     wait_vmcnt<63, true>();
     asm volatile("" ::: "memory");
@@ -484,6 +513,13 @@ template <int EPI>
 static hipError_t launch_pipe2(const GemmParams& p, hipStream_t s) {
   const int64_t tiles = ((p.m + 255) / 256) * ((p.n + 255) / 256);
   fp8_gemm_pipe2<EPI><<<dim3((unsigned)tiles), dim3(256), 0, s>>>(p);
+  return hipGetLastError();
+}
+
+template <int EPI>
+static hipError_t launch_pipe2s(const GemmParams& p, hipStream_t s) {
+  const int64_t tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128);
+  fp8_gemm_pipe2s<EPI><<<dim3((unsigned)tiles), dim3(256), 0, s>>>(p);
   return hipGetLastError();
 }
 
@@ -517,11 +553,12 @@ static hipError_t launch_cfg(const GemmParams& p, hipStream_t s) {
 // 5 = 256x128 (2x2), 6 = 256x256 (4x2: two waves per SIMD),
 // 7 = 256x256 (2x4: two waves per SIMD), 8 = 256x256 pipelined (2x2),
 // 9 = 256x256 pipelined (2x4), 10 = 256x256 two-slot pipelined, 128-byte stages,
-// 11 = tile 10 as a persistent kernel (one workgroup per CU).
+// 11 = tile 10 as a persistent kernel (one workgroup per CU),
+// 12 = 128x128 two-slot pipelined (2x2 waves of 64x64, two workgroups per CU).
 int pick_tile(const GemmParams& p) {
   auto tiles = [&](int bm, int bn) { return ((p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn); };
   if (tiles(256, 256) >= 512) return 10;
-  if (tiles(128, 128) >= 256) return 2;
+  if (tiles(128, 128) >= 256) return 12;
   return 3;
 }
 
@@ -541,6 +578,7 @@ hipError_t launch_epi(const GemmParams& p, int tile, hipStream_t s) {
     case 9: return launch_pipe<2, 4, EPI>(p, s);
     case 10: return launch_pipe2<EPI>(p, s);
     case 11: return launch_persist<EPI>(p, s);
+    case 12: return launch_pipe2s<EPI>(p, s);
     default: return hipErrorInvalidValue;
   }
 }

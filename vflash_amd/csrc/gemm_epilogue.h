@@ -4,6 +4,8 @@
 #include "common.h"
 #include "gemm_params.h"
 
+#include <type_traits>
+
 namespace vfa {
 
 // Logical tile index for this workgroup.  Workgroup b is dispatched to XCD
@@ -42,11 +44,37 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group_
 // Phase 2 (whole workgroup): each thread moves 16-byte row chunks from LDS to
 // global memory with coalesced 16-byte stores, applying the gate-residual
 // epilogue there with coalesced residual loads.
-template <int BM, int BN, int WGM, int WGN, int EPI>
+// LDS bytes of the staged tile vectors: weight scales (or the one scalar),
+// activation row scales, bias.
+constexpr int VEC_LDS = 3 * 1024;
+
+// Copy the scale and bias vectors of a BM x BN tile into LDS (vec_lds) with
+// buffer-load-to-LDS DMA, one instruction each on waves 0, 1 and 2.  Issued
+// with the tile's first K stage, so the caller's first DMA wait and barrier
+// also cover these; entries past the matrix edge read as zero.
+template <int BM, int BN>
+__device__ __forceinline__ void stage_vectors(const GemmParams& p, int64_t m0, int64_t n0,
+                                              int wave, int lane, uint32_t vec_lds) {
+  static_assert(BM * 4 <= 1024 && BN * 4 <= 1024, "vector slots hold 256 entries");
+  if (wave == 0) {
+    const uint32_t bytes = p.sw_step ? (uint32_t)(min((int64_t)BN, p.n - n0) * 4) : 4u;
+    lds_dma16(make_rsrc(p.sw + (p.sw_step ? n0 : 0), bytes), vec_lds, (uint32_t)lane * 16);
+  } else if (wave == 1) {
+    lds_dma16(make_rsrc(p.sa + m0, (uint32_t)(min((int64_t)BM, p.m - m0) * 4)), vec_lds + 1024,
+              (uint32_t)lane * 16);
+  } else if (wave == 2 && p.bias) {
+    lds_dma16(make_rsrc(p.bias + n0, (uint32_t)(min((int64_t)BN, p.n - n0) * 2)),
+              vec_lds + 2048, (uint32_t)lane * 16);
+  }
+}
+
+// VEC: read the scale and bias vectors from the LDS copy `vec` made by
+// stage_vectors (true), or from global memory (false).
+template <int BM, int BN, int WGM, int WGN, int EPI, bool VEC = false>
 __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
                                               v16f (&acc)[BN / WGN / 32][BM / WGM / 32],
                                               int64_t m0, int64_t n0, int wm, int wn, int tid,
-                                              uint8_t* stage) {
+                                              uint8_t* stage, const uint8_t* vec = nullptr) {
   constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
   constexpr int NT = 64 * WGM * WGN;
   constexpr int CH = BN / 8;  // 16-byte chunks per staged row
@@ -61,69 +89,94 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
   static_for<MB>([&](auto i) { static_for<NG>([&](auto j) { rmax[i][j] = 0.0f; }); });
   float sam[MB];
   static_for<MB>([&](auto mb) {
-    const int64_t m = m0 + wm * WM + mb * 32 + fr;
-    sam[mb] = m < p.m ? sa_p[m] : 0.0f;
+    const int row = wm * WM + mb * 32 + fr;
+    if constexpr (VEC) {
+      sam[mb] = reinterpret_cast<const float*>(vec + 1024)[row];
+    } else {
+      sam[mb] = m0 + row < p.m ? sa_p[m0 + row] : 0.0f;
+    }
   });
+  const bool sw_vector = p.sw_step != 0;
+  const float sw0 = VEC ? reinterpret_cast<const float*>(vec)[0] : 0.0f;
 
-  // Column-block major: the scale and bias of one 32-column block (4 columns
-  // per g for this lane) are live while its MB row blocks are written.  All
-  // phase-1 stores go to LDS, so these global loads never wait on them.
-  static_for<NB>([&](auto nb) {
-    float sv[4][4], bv[4][4];
-    static_for<4>([&](auto g) {
-      const int64_t n = n0 + wn * WN + nb * 32 + g * 8 + fh * 4;
-      const bool ok = n < p.n;
-      static_for<4>([&](auto i) {
-        sv[g][i] = ok ? sw_p[(n + i) * p.sw_step] : 0.0f;
-        bv[g][i] = (ok && bias_p) ? bf16_to_f32(bias_p[n + i]) : 0.0f;
-      });
-    });
-    static_for<MB>([&](auto mb) {
-      const int row = wm * WM + mb * 32 + fr;  // tile row
-      const int64_t m = m0 + row;
-      const bool mvalid = m < p.m;
-      v16f d = v16f{};
-      if constexpr (EPI == EPI_LORA) {
-        // delta block = B[n, :] . t[m, :] on bf16 MFMA, binary32 accumulate.
-        const int64_t nrow = n0 + wn * WN + nb * 32 + fr;
-        const bool nok = nrow < p.n;
-        for (int r = 0; r < p.rank; r += 16) {
-          v8s bfr = v8s{}, tfr = v8s{};
-          if (nok) bfr = *reinterpret_cast<const v8s*>(p.lora_b + nrow * p.ldb + r + fh * 8);
-          if (mvalid) tfr = *reinterpret_cast<const v8s*>(p.lora_t + m * p.ldt + r + fh * 8);
-          d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, bfr),
-                                                      __builtin_bit_cast(v8bf, tfr), d, 0, 0,
-                                                      0);
-        }
-      }
+  // Phase 1, column-block major: the scale and bias of one 32-column block (4
+  // columns per g for this lane) are live while its MB row blocks are written.
+  // Two copies (with and without bias) keep the bias test out of the loop.
+  auto phase1 = [&](auto has_bias) {
+    static_for<NB>([&](auto nb) {
+      float sv[4][4], bv[4][4];
       static_for<4>([&](auto g) {
-        uint32_t w[2];
-        // Output pairs: every bf16 rounding is one v_cvt_pk_bf16_f32 for two values.
-        static_for<2>([&](auto h) {
-          constexpr int i0 = 2 * h, i1 = 2 * h + 1;
-          uint32_t pw = pack_bf16x2(acc[nb][mb][g * 4 + i0] * sam[mb] * sv[g][i0],
-                                    acc[nb][mb][g * 4 + i1] * sam[mb] * sv[g][i1]);
-          if (bias_p) pw = pack_bf16x2(bf16_lo(pw) + bv[g][i0], bf16_hi(pw) + bv[g][i1]);
-          if constexpr (EPI == EPI_GELU) {
-            pw = pack_bf16x2(gelu_tanh(bf16_lo(pw)), gelu_tanh(bf16_hi(pw)));
-            rmax[mb][nb / 2] =
-                fmaxf(rmax[mb][nb / 2], fmaxf(fabsf(bf16_lo(pw)), fabsf(bf16_hi(pw))));
-          } else if constexpr (EPI == EPI_LORA) {
-            uint32_t dp = pack_bf16x2(d[g * 4 + i0], d[g * 4 + i1]);
-            if (p.lora_scale != 1.0f)
-              dp = pack_bf16x2(bf16_lo(dp) * p.lora_scale, bf16_hi(dp) * p.lora_scale);
-            if (p.lora_strength != 1.0f)
-              dp = pack_bf16x2(bf16_lo(dp) * p.lora_strength, bf16_hi(dp) * p.lora_strength);
-            pw = pack_bf16x2(bf16_lo(pw) + bf16_lo(dp), bf16_hi(pw) + bf16_hi(dp));
+        const int col = wn * WN + nb * 32 + g * 8 + fh * 4;  // tile column of value i = 0
+        if constexpr (VEC) {
+          const v4f s4 = *reinterpret_cast<const v4f*>(vec + col * 4);
+          uint2 b4 = make_uint2(0u, 0u);
+          if constexpr (has_bias) b4 = *reinterpret_cast<const uint2*>(vec + 2048 + col * 2);
+          static_for<4>([&](auto i) {
+            sv[g][i] = sw_vector ? s4[(int)i] : sw0;
+            const uint32_t bw = i < 2 ? b4.x : b4.y;
+            bv[g][i] = i % 2 ? bf16_hi(bw) : bf16_lo(bw);
+          });
+        } else {
+          const int64_t n = n0 + col;
+          const bool ok = n < p.n;
+          static_for<4>([&](auto i) {
+            sv[g][i] = ok ? sw_p[(n + i) * p.sw_step] : 0.0f;
+            bv[g][i] = (ok && has_bias) ? bf16_to_f32(bias_p[n + i]) : 0.0f;
+          });
+        }
+      });
+      static_for<MB>([&](auto mb) {
+        const int row = wm * WM + mb * 32 + fr;  // tile row
+        const int64_t m = m0 + row;
+        const bool mvalid = m < p.m;
+        v16f d = v16f{};
+        if constexpr (EPI == EPI_LORA) {
+          // delta block = B[n, :] . t[m, :] on bf16 MFMA, binary32 accumulate.
+          const int64_t nrow = n0 + wn * WN + nb * 32 + fr;
+          const bool nok = nrow < p.n;
+          for (int r = 0; r < p.rank; r += 16) {
+            v8s bfr = v8s{}, tfr = v8s{};
+            if (nok) bfr = *reinterpret_cast<const v8s*>(p.lora_b + nrow * p.ldb + r + fh * 8);
+            if (mvalid) tfr = *reinterpret_cast<const v8s*>(p.lora_t + m * p.ldt + r + fh * 8);
+            d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, bfr),
+                                                        __builtin_bit_cast(v8bf, tfr), d, 0, 0,
+                                                        0);
           }
-          w[h] = pw;
+        }
+        static_for<4>([&](auto g) {
+          uint32_t w[2];
+          // Output pairs: every bf16 rounding is one v_cvt_pk_bf16_f32 for two values.
+          static_for<2>([&](auto h) {
+            constexpr int i0 = 2 * h, i1 = 2 * h + 1;
+            uint32_t pw = pack_bf16x2(acc[nb][mb][g * 4 + i0] * sam[mb] * sv[g][i0],
+                                      acc[nb][mb][g * 4 + i1] * sam[mb] * sv[g][i1]);
+            if constexpr (has_bias)
+              pw = pack_bf16x2(bf16_lo(pw) + bv[g][i0], bf16_hi(pw) + bv[g][i1]);
+            if constexpr (EPI == EPI_GELU) {
+              pw = pack_bf16x2(gelu_tanh(bf16_lo(pw)), gelu_tanh(bf16_hi(pw)));
+              rmax[mb][nb / 2] =
+                  fmaxf(rmax[mb][nb / 2], fmaxf(fabsf(bf16_lo(pw)), fabsf(bf16_hi(pw))));
+            } else if constexpr (EPI == EPI_LORA) {
+              uint32_t dp = pack_bf16x2(d[g * 4 + i0], d[g * 4 + i1]);
+              if (p.lora_scale != 1.0f)
+                dp = pack_bf16x2(bf16_lo(dp) * p.lora_scale, bf16_hi(dp) * p.lora_scale);
+              if (p.lora_strength != 1.0f)
+                dp = pack_bf16x2(bf16_lo(dp) * p.lora_strength, bf16_hi(dp) * p.lora_strength);
+              pw = pack_bf16x2(bf16_lo(pw) + bf16_lo(dp), bf16_hi(pw) + bf16_hi(dp));
+            }
+            w[h] = pw;
+          });
+          const int c = (wn * WN + nb * 32 + g * 8) / 8;  // 16-byte chunk of the row
+          *reinterpret_cast<uint2*>(stage + row * PITCH + ((c ^ (row % CH)) << 4) + fh * 8) =
+              make_uint2(w[0], w[1]);
         });
-        const int c = (wn * WN + nb * 32 + g * 8) / 8;  // 16-byte chunk of the row
-        *reinterpret_cast<uint2*>(stage + row * PITCH + ((c ^ (row % CH)) << 4) + fh * 8) =
-            make_uint2(w[0], w[1]);
       });
     });
-  });
+  };
+  if (bias_p)
+    phase1(std::true_type{});
+  else
+    phase1(std::false_type{});
 
   if constexpr (EPI == EPI_GELU) {
     static_assert(NB % 2 == 0, "GELU epilogue needs 64-column wave groups");
@@ -141,40 +194,53 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
   }
   __syncthreads();
 
-  // Phase 2: LDS rows -> global, 16 bytes per thread per step.
-  const bool vec_out = ((reinterpret_cast<uintptr_t>(p.out) & 15) == 0) && (p.ldo % 8 == 0) &&
-                       (p.plane_cols == 0 || p.plane_stride % 8 == 0);
-  for (int q = tid; q < BM * CH; q += NT) {
-    const int row = q / CH, c = q % CH;
-    const int64_t m = m0 + row, n = n0 + c * 8;
-    if (m >= p.m || n >= p.n) continue;
-    v4i v = *reinterpret_cast<const v4i*>(stage + row * PITCH + ((c ^ (row % CH)) << 4));
-    if constexpr (EPI == EPI_GATE) {
-      const uint16_t* res = p.residual + m * p.ldr + n;
-      const uint16_t* gt = p.gate + m * p.gate_ts + n * p.gate_hs;
+  // Phase 2: LDS rows -> global.  Thread tid owns the 16-byte column chunk
+  // c = tid % CH of rows tid / CH + RPP * it, so its column, plane and
+  // bounds are computed once.
+  constexpr int RPP = NT / CH;  // rows per pass
+  static_assert(NT % CH == 0 && BM % RPP == 0, "whole phase-2 passes");
+  const int c = tid % CH, r0 = tid / CH;
+  const int64_t n = n0 + c * 8;
+  if (n >= p.n) return;
+  const int rows = (int)min((int64_t)BM, p.m - m0);
+  uint16_t* base = p.out + n;
+  if (p.plane_cols > 0) {
+    const int64_t plane = n / p.plane_cols;
+    base = p.out + plane * p.plane_stride + (n - plane * p.plane_cols);
+  }
+  auto pass = [&](auto vec_out) {
+#pragma unroll 8
+    for (int it = 0; it < BM / RPP; ++it) {
+      const int row = r0 + it * RPP;
+      if (row >= rows) break;
+      const int64_t m = m0 + row;
+      v4i v = *reinterpret_cast<const v4i*>(stage + row * PITCH + ((c ^ (row % CH)) << 4));
+      if constexpr (EPI == EPI_GATE) {
+        const uint16_t* res = p.residual + m * p.ldr + n;
+        const uint16_t* gt = p.gate + m * p.gate_ts + n * p.gate_hs;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t y = (uint32_t)v[j];
-        const uint32_t gy = pack_bf16x2(bf16_to_f32(gt[(2 * j) * p.gate_hs]) * bf16_lo(y),
-                                        bf16_to_f32(gt[(2 * j + 1) * p.gate_hs]) * bf16_hi(y));
-        v[j] = (int)pack_bf16x2(bf16_to_f32(res[2 * j]) + bf16_lo(gy),
-                                bf16_to_f32(res[2 * j + 1]) + bf16_hi(gy));
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t y = (uint32_t)v[j];
+          const uint32_t gy = pack_bf16x2(bf16_to_f32(gt[(2 * j) * p.gate_hs]) * bf16_lo(y),
+                                          bf16_to_f32(gt[(2 * j + 1) * p.gate_hs]) * bf16_hi(y));
+          v[j] = (int)pack_bf16x2(bf16_to_f32(res[2 * j]) + bf16_lo(gy),
+                                  bf16_to_f32(res[2 * j + 1]) + bf16_hi(gy));
+        }
+      }
+      uint16_t* dst = base + m * p.ldo;
+      if constexpr (vec_out) {
+        *reinterpret_cast<v4i*>(dst) = v;
+      } else {
+        reinterpret_cast<uint2*>(dst)[0] = make_uint2((uint32_t)v[0], (uint32_t)v[1]);
+        reinterpret_cast<uint2*>(dst)[1] = make_uint2((uint32_t)v[2], (uint32_t)v[3]);
       }
     }
-    uint16_t* dst;
-    if (p.plane_cols > 0) {
-      const int64_t plane = n / p.plane_cols;
-      dst = p.out + plane * p.plane_stride + m * p.ldo + (n - plane * p.plane_cols);
-    } else {
-      dst = p.out + m * p.ldo + n;
-    }
-    if (vec_out) {
-      *reinterpret_cast<v4i*>(dst) = v;
-    } else {
-      reinterpret_cast<uint2*>(dst)[0] = make_uint2((uint32_t)v[0], (uint32_t)v[1]);
-      reinterpret_cast<uint2*>(dst)[1] = make_uint2((uint32_t)v[2], (uint32_t)v[3]);
-    }
-  }
+  };
+  if (((reinterpret_cast<uintptr_t>(p.out) & 15) == 0) && (p.ldo % 8 == 0) &&
+      (p.plane_cols == 0 || p.plane_stride % 8 == 0))
+    pass(std::true_type{});
+  else
+    pass(std::false_type{});
 }
 
 }  // namespace vfa

@@ -238,6 +238,7 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
 __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t ring[FP4_LDS];
+  __shared__ __attribute__((aligned(1024))) uint8_t vec[VEC_LDS];
   constexpr int MB = 4, NB = 4;
   const int tiles_m = (int)((p.m + 255) / 256), tiles_n = (int)((p.n + 255) / 256);
   int tm, tn;
@@ -353,6 +354,7 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
   using I3 = std::integral_constant<int, 3>;
 
   Raw r0, r1;
+  stage_vectors<256, 256>(p, m0, n0, wave, lane, __builtin_amdgcn_readfirstlane(lds_addr(vec)));
   issue(0, 0);
   issue(1, 1);
   wait_vmcnt<0, true>();
@@ -382,7 +384,7 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
   wait_vmcnt<0, true>();  // every DMA has landed before the ring becomes the staging tile
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  gemm_epilogue<256, 256, 2, 2, EPI_BIAS>(p, acc, m0, n0, wm, wn, (int)threadIdx.x, ring);
+  gemm_epilogue<256, 256, 2, 2, EPI_BIAS, true>(p, acc, m0, n0, wm, wn, (int)threadIdx.x, ring, vec);
 }
 
 hipError_t launch_nvfp4_gemm(const Fp4Params& p, int tile, hipStream_t s) {
