@@ -46,6 +46,8 @@ def parse():
     )
     p.add_argument("--skinny-m", type=int, default=1024)
     p.add_argument("--skinny-n", type=int, default=6144)
+    p.add_argument("--operand-sets", type=int, default=0,
+                   help="rotating operand sets for the small shapes (0 = enough to exceed the last-level cache)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--tile", type=int, default=0, help="force a GEMM tile configuration")
     p.add_argument("--group-m", type=int, default=0)
@@ -190,7 +192,7 @@ def make_workload(args, dev):
     if wl in ("fp8_linear", "small", "qkv"):
         m, k, n = {"fp8_linear": (32760, 5120, 13824), "small": (4096, 3072, 3072),
                    "qkv": (32760, 5120, 15360)}[wl]
-        host, sets = linear_sets(m, k, n, 8 if wl == "small" else 1, dev)
+        host, sets = linear_sets(m, k, n, (args.operand_sets or 8) if wl == "small" else 1, dev)
         ex = RowFP8Execution("w8a8", activation_quantizer="hip")
         # One call through the module API checks the drop-in path end to end; the
         # timed step is the same pair of launches that RowFP8Execution.linear makes.
@@ -275,7 +277,7 @@ def make_workload(args, dev):
     if wl == "skinny":
         m, k, n, r = args.skinny_m, 1536, args.skinny_n, 32
         per_set = m * k * 3 + n * k + 2 * m * n + 2 * r * (k + n) + 2 * m * r
-        count = max(2, int(600e6 // per_set) + 1)  # > 2x the last-level cache
+        count = args.operand_sets or max(2, int(600e6 // per_set) + 1)  # > 2x the last-level cache
         sets = []
         for seed in range(count):
             x, codes, scale, b = seeded_linear(m, k, n, bias=True, seed=seed)

@@ -96,6 +96,27 @@ int vflash_fp8_linear_gelu(const void* a, const float* sa, int64_t lda, const vo
 int64_t vflash_row_parts(int64_t n);
 
 /*
+ * FFN input projection with the SwiGLU epilogue (the H3 feed-forward input).
+ * Replaces RowFP8Execution.linear on the packed projection followed by
+ * value * silu(gate) (src/vflash/native/h3_native_denoiser.py:369-376) or its
+ * fused form triton_strict_bf16_silu_mul (src/vflash/native/h3_fused_ops.py:184-224,
+ * 660-700).  w holds n = 2F rows: rows [0, F) give the value columns and rows
+ * [F, 2F) the gate columns of the packed output, as .chunk(2, dim=-1) splits it.
+ *   p   = bf16(bf16(acc * sa * sw) + bias)            (the packed [m, 2F] output)
+ *   h   = bf16(p[:, f] * bf16(silu(p[:, F + f])))     written to h [m, F] (ldh)
+ *   amax_part fp32 [m, vflash_swiglu_parts(n)]: max |h| of each row over each
+ *   128-column group, consumed by vflash_requant_rows_e4m3.
+ *   Requires n % 256 == 0, ldh % 8 == 0, h and sw (and bias) 16-byte aligned.
+ */
+int vflash_fp8_linear_swiglu(const void* a, const float* sa, int64_t lda, const void* w,
+                             const float* sw, int64_t ldw, int64_t m, int64_t n, int64_t k,
+                             const void* bias, void* h, int64_t ldh, float* amax_part,
+                             void* stream);
+
+/* Number of 128-column groups per row in the SwiGLU amax_part: ceil(n / 2 / 128). */
+int64_t vflash_swiglu_parts(int64_t n);
+
+/*
  * Per-token E4M3 requantization from epilogue row maxima.
  * Same arithmetic as vflash_quantize_rows_e4m3 (the down projection's own
  * activation quantization, src/vflash/native/h3_fp8_linear.py:102-108), with

@@ -88,6 +88,20 @@ def gelu_tanh(y) -> np.ndarray:
     return bf16_round(F32(0.5) * y * (F32(1.0) + np.tanh(inner)))
 
 
+def silu_mul(packed) -> np.ndarray:
+    """H3 SwiGLU activation of a packed bf16 [.., 2F] projection output:
+    value, gate = packed.chunk(2, -1); bf16(value * bf16(silu(gate))) with
+    silu(g) = g / (1 + exp(-g)) in binary32 (h3_native_denoiser.py:369-373 with
+    eager bf16 tensors; the fused kernel h3_fused_ops.py:184-224 keeps the same
+    two roundings).  Pinned against torch's eager bf16 value * F.silu(gate)."""
+    packed = np.asarray(packed, F32)
+    f = packed.shape[-1] // 2
+    value, gate = packed[..., :f], packed[..., f:]
+    with np.errstate(over="ignore"):
+        act = bf16_round(gate / (F32(1.0) + np.exp(-gate)))
+        return bf16_round(value * act)
+
+
 def gate_residual(residual, gate, y) -> np.ndarray:
     """bf16(residual + bf16(gate * y)) in binary32 (h3_fused_ops.py:153-170)."""
     gated = bf16_round(np.asarray(gate, F32) * np.asarray(y, F32))
@@ -112,12 +126,15 @@ def lora_merge(base, delta) -> np.ndarray:
     return bf16_round(np.asarray(base, F32) + np.asarray(delta, F32))
 
 
-def ffn(x, up_codes, up_scale, up_bias, down_codes, down_scale, down_bias, gate, residual):
-    """The FFN chain of this path: up + bias, GELU-tanh, per-token requant,
-    down + bias, gate-residual.  Returns (g, h_codes, h_scales, out)."""
+def ffn(x, up_codes, up_scale, up_bias, down_codes, down_scale, down_bias, gate, residual,
+        activation: str = "gelu_tanh"):
+    """The FFN chain of this path: up + bias, activation (GELU-tanh, or the H3
+    SwiGLU on a packed [2F, H] up projection), per-token requant, down + bias,
+    gate-residual.  Returns (g, h_codes, h_scales, out)."""
     x = np.asarray(x, F32)
     m = x.shape[0]
-    g = gelu_tanh(w8a8_linear(x, up_codes, up_scale, up_bias))
+    up = w8a8_linear(x, up_codes, up_scale, up_bias)
+    g = silu_mul(up) if activation == "swiglu" else gelu_tanh(up)
     h_codes, h_scales = quantize_rows(g)
     y = add_bias(scaled_mm(h_codes[:m], h_scales[:m], down_codes, down_scale), down_bias)
     return g, h_codes, h_scales, gate_residual(residual, gate, y)

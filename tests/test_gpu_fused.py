@@ -1,4 +1,4 @@
-"""Merged QKV, the GELU-tanh FFN chain and the LoRA linear on gfx950 vs the oracle."""
+"""Merged QKV, the GELU-tanh and SwiGLU FFN chains and the LoRA linear on gfx950 vs the oracle."""
 
 import numpy as np
 import pytest
@@ -157,6 +157,76 @@ def test_ffn_config_shape_sampled(dev):
                       sd.reshape(-1).numpy(), bd.float().numpy(), gate.float().numpy(),
                       res.float().numpy()[rows])
     assert chain_error(got, chain) <= 1e-2
+
+
+def within_one_ulp(got, ref):
+    """|got - ref| <= one bf16 step of ref, elementwise (plus the bf16 subnormal step)."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return np.abs(got - ref) <= np.abs(ref) * 2.0**-7 + 2.0**-133
+
+
+@pytest.mark.parametrize("m,h,f,token_gate", [(300, 512, 512, False), (77, 256, 384, True)])
+def test_swiglu_ffn_chain_stages_against_the_oracle(dev, m, h, f, token_gate):
+    # H3 FFN: packed input projection [2F, H] (values, then gates), SwiGLU, requant,
+    # output projection [H, F] with the gate-residual epilogue.
+    x, cu, su, bu, cd, sd, bd, gate, res = ffn_inputs(m, h, 2 * f, token_gate=token_gate)
+    # The output projection maps the F activations back to H.
+    cd, sd = quantize_weight_rows(torch.randn((h, f), generator=torch.Generator().manual_seed(9)) * 0.02)
+    d = lambda t: t.to(dev)
+    a, sa = kernels.quantize_rows(d(x))
+    hh, amax = kernels.fp8_gemm_swiglu(a, sa, d(cu), d(su), m, d(bu))
+    h_np = hh.float().cpu().numpy()
+    # Stage 1a: the packed projection inside the SwiGLU tile equals the plain
+    # linear (same K order), so SwiGLU of the plain kernel's output pins the epilogue.
+    packed = kernels.fp8_gemm(a, sa, d(cu), d(su), m, d(bu)).float().cpu().numpy()
+    ref_h = O.silu_mul(packed)
+    assert np.all(within_one_ulp(h_np, ref_h)) and (h_np != ref_h).mean() < 5e-3
+    # Stage 1b: the packed projection against the oracle (tolerance), and SwiGLU of it.
+    ref_lin = O.w8a8_linear(x.float().numpy(), u8(cu), su.reshape(-1).numpy(), bu.float().numpy())
+    rel_check(packed, ref_lin)
+    # Row maxima: exact maxima of |h| per 128-column group.
+    assert np.array_equal(amax.cpu().numpy(), np.abs(h_np).reshape(m, -1, 128).max(axis=2))
+    # Stage 2: requantization bit-exact on the kernel's own h.
+    hc, hs = kernels.requant_rows(hh, amax)
+    rc, rs = O.quantize_rows(h_np)
+    assert np.array_equal(u8(hc), rc) and np.array_equal(hs.reshape(-1).cpu().numpy(), rs)
+    # Stage 3: output projection with gate-residual on the same codes.
+    out = kernels.fp8_gemm_gate_residual(hc, hs, d(cd), d(sd), m, d(gate), d(res), d(bd))
+    y = O.add_bias(O.scaled_mm(rc[:m], rs[:m], u8(cd), sd.reshape(-1).numpy()), bd.float().numpy())
+    rel_check(out.float().cpu().numpy(), O.gate_residual(res.float().numpy(), gate.float().numpy(), y))
+    # Whole chain through the module-level composition vs the oracle chain.
+    ex = RowFP8Execution("w8a8", activation_quantizer="triton")
+    full = fp8_ffn(ex, d(x), d(cu), d(su), d(bu), d(cd), d(sd), d(bd), d(gate), d(res),
+                   activation="swiglu")
+    assert torch.equal(full, out)
+    *_, chain = O.ffn(x.float().numpy(), u8(cu), su.reshape(-1).numpy(), bu.float().numpy(),
+                      u8(cd), sd.reshape(-1).numpy(), bd.float().numpy(), gate.float().numpy(),
+                      res.float().numpy(), activation="swiglu")
+    assert chain_error(full.float().cpu().numpy(), chain) <= 1e-2
+
+
+def test_swiglu_h3_shape_sampled(dev):
+    # H3 feed-forward: hidden 5376, inner 14336 (packed input projection [28672, 5376]).
+    m, h, f = 32760, 5376, 14336
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn((m, h), generator=g).to(torch.bfloat16)
+    cu, su = quantize_weight_rows(torch.randn((2 * f, h), generator=g) * 0.02)
+    bu = (torch.randn(2 * f, generator=g) * 0.01).to(torch.bfloat16)
+    d = lambda t: t.to(dev)
+    a, sa = kernels.quantize_rows(d(x))
+    hh, amax = kernels.fp8_gemm_swiglu(a, sa, d(cu), d(su), m, d(bu))
+    rows = np.r_[0:8, 16380:16388, 32752:32760]
+    h_np = hh.float().cpu().numpy()[rows]
+    ref_lin = O.w8a8_linear(x.float().numpy()[rows], u8(cu), su.reshape(-1).numpy(), bu.float().numpy())
+    ref_h = O.silu_mul(ref_lin)
+    # Tolerance: value and gate each within the GEMM bound, composed through one product.
+    err = np.abs(h_np.astype(np.float64) - ref_h)
+    rms = float(np.sqrt(np.mean(ref_h.astype(np.float64) ** 2)))
+    assert np.all(err <= 2.0**-5 * np.abs(ref_h) + 1e-2 * rms)
+    assert (err > 1e-2 * np.abs(ref_h) + 1e-2 * rms).mean() <= 1e-3
+    assert np.array_equal(amax.cpu().numpy()[rows], np.abs(h_np).reshape(len(rows), -1, 128).max(axis=2))
+    assert bool(torch.isfinite(hh.float()).all())
 
 
 @pytest.mark.parametrize("m,n", [(256, 1536), (512, 4608), (1024, 6144)])

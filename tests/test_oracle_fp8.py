@@ -117,6 +117,33 @@ def test_gelu_oracle_tracks_torch_on_every_bf16_value():
     assert O.gelu_tanh(np.float32([-30.0]))[0] == 0
 
 
+def test_silu_mul_oracle_tracks_torch_eager_bf16_on_every_gate_value():
+    # H3's _silu_mul on bf16 tensors: value * F.silu(gate), each op rounding to bf16.
+    from oracle.formats import bf16_from_bits
+
+    g = bf16_from_bits(np.arange(65536, dtype=np.uint32).astype(np.uint16))
+    g = g[np.isfinite(g)]
+    rng = np.random.default_rng(11)
+    v = bf16_round(rng.standard_normal(g.size) * 4)
+    ours = O.silu_mul(np.stack([v, g], -1).reshape(-1, 2))
+    tv = torch.from_numpy(v).to(torch.bfloat16).reshape(-1, 1)
+    tg = torch.from_numpy(g).to(torch.bfloat16).reshape(-1, 1)
+    ref = (tv * torch.nn.functional.silu(tg)).float().numpy()
+    # Different binary32 exp implementations may flip the rounding of silu by one
+    # bf16 step, which the product then carries.
+    with np.errstate(invalid="ignore"):
+        close = (ours == ref) | (np.abs(ours - ref) <= np.abs(ref) * 2.0**-6 + 2.0**-133)
+    assert np.all(close)
+    assert (ours != ref).mean() < 2e-3
+    # Closed forms: silu(0) = 0; silu(g) -> g for large g and -> -0 for large -g.
+    assert O.silu_mul(np.float32([[3.0, 0.0]]))[0, 0] == 0
+    assert O.silu_mul(np.float32([[1.0, 100.0]]))[0, 0] == 100.0
+    assert O.silu_mul(np.float32([[1.0, -200.0]]))[0, 0] == 0
+    # chunk(2, -1): values are the first half of the packed row.
+    packed = np.float32([[1.0, 2.0, 0.0, 50.0]])
+    assert np.array_equal(O.silu_mul(packed), np.float32([[0.0, 100.0]]))
+
+
 def test_gate_residual_matches_torch_eager_bf16():
     rng = np.random.default_rng(5)
     res = bf16_round(rng.standard_normal((33, 70)))

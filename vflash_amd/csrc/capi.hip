@@ -87,7 +87,7 @@ const char* vflash_status_string(int s) {
 
 int vflash_set_gemm_tile(int tile, int group_m) {
   const int prev = g_tile;
-  if (tile >= 0 && tile <= 12) g_tile = tile;
+  if (tile >= 0 && tile <= 14) g_tile = tile;
   g_group_m = group_m > 0 ? group_m : 8;
   return prev;
 }
@@ -137,6 +137,22 @@ int vflash_fp8_linear_gelu(const void* a, const float* sa, int64_t lda, const vo
   vfa::GemmParams p = base_params(a, sa, lda, w, sw, ldw, m, n, k, bias, g, ldg);
   p.amax_part = amax_part;
   return status(vfa::launch_fp8_gemm(p, vfa::EPI_GELU, static_cast<hipStream_t>(stream)));
+}
+
+int64_t vflash_swiglu_parts(int64_t n) { return n > 0 ? (n / 2 + 127) / 128 : 0; }
+
+int vflash_fp8_linear_swiglu(const void* a, const float* sa, int64_t lda, const void* w,
+                             const float* sw, int64_t ldw, int64_t m, int64_t n, int64_t k,
+                             const void* bias, void* h, int64_t ldh, float* amax_part,
+                             void* stream) {
+  if (!gemm_args_ok(a, sa, lda, w, sw, ldw, m, n, k, bias)) return VFLASH_EINVAL;
+  if (n % 256 || !h || !amax_part || ldh < n / 2 || ldh % 8 || !aligned(h, 16) ||
+      !aligned(amax_part, 4) || !aligned(sw, 16) || (bias && !aligned(bias, 16)))
+    return VFLASH_EINVAL;
+  vfa::GemmParams p = base_params(a, sa, lda, w, sw, ldw, m, n, k, bias, h, ldh);
+  p.half_n = n / 2;
+  p.amax_part = amax_part;
+  return status(vfa::launch_fp8_gemm(p, vfa::EPI_SWIGLU, static_cast<hipStream_t>(stream)));
 }
 
 int vflash_requant_rows_e4m3(const void* g, int64_t m, int64_t k, int64_t ldg,

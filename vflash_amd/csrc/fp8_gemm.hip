@@ -15,6 +15,9 @@
 //   EPI_LORA   out = bf16(base + delta), delta = bf16(t . B^T) with the optional
 //              bf16(delta * scale), bf16(delta * strength) steps
 //              (adapters/h3_reference_lora.py:75-90)
+//   EPI_SWIGLU h = bf16(value * bf16(silu(gate))) with value = base[:, f] and
+//              gate = base[:, half_n + f], plus per-row |h| maxima per 128
+//              columns (h3_native_denoiser.py:369-376, h3_fused_ops.py:184-224)
 //
 // Tiling: a workgroup of WGM x WGN waves computes a BM x BN tile; each wave
 // owns (BM/WGM) x (BN/WGN) as 32x32 blocks of v_mfma_f32_32x32x64_f8f6f4.
@@ -291,10 +294,12 @@ __global__ void __launch_bounds__(64 * WGM * WGN) fp8_gemm_pipe(const GemmParams
 // The DMA of a stage is issued about one stage of MFMA work before it is
 // needed; rows are stored with the lds_swizzle chunk permutation.
 // Ring bytes of the two-slot pipeline for a BT x BT tile (BT = 256 or 128).
-constexpr int pipe2_lds(int bt) { return 2 * 2 * bt * 128; }
+constexpr int pipe2_lds(int bt, int ns = 2) { return ns * 2 * bt * 128; }
 constexpr int PIPE2_LDS = pipe2_lds(256);  // two 64 KB stage slots
 
-template <int EPI, int BT = 256>
+// NS stage slots: the DMA of stage kt + NS is issued once stage kt is read,
+// so NS - 1 stages are in flight while one is multiplied.
+template <int EPI, int BT = 256, int NS = 2>
 __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, uint8_t* ring,
                                            uint32_t ring_lds, uint8_t* vec, uint32_t vec_lds,
                                            int wave) {
@@ -304,10 +309,11 @@ __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, 
   constexpr int SLOT = 2 * HALF;
   constexpr int DMA_A = HALF / 1024 / 4;   // one-KB DMA instructions per wave per operand
   constexpr int DMA = 2 * DMA_A;           // per wave per stage
-  static_assert(2 * SLOT == pipe2_lds(BT), "slot layout");
+  static_assert(NS * SLOT == pipe2_lds(BT, NS), "slot layout");
+  static_assert(NS >= 2 && (NS - 1) * DMA < 64, "vmcnt range");
   static_assert(DMA_A % 2 == 0, "A blocks alternate between the two swizzle parities");
 
-  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * (EPI == EPI_SWIGLU ? BN / 2 : BN);
   // The lane index comes from mbcnt and the wave index arrives as a scalar, so
   // in the persistent form no per-lane value stays live across tiles (holding
   // the work-item id there costs a spill whose reload drains the stores).
@@ -318,9 +324,22 @@ __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, 
   const int wm = wave % WGM, wn = wave / WGM;
 
   const int64_t rows_a = min((int64_t)BM, p.m - m0);
-  const int64_t rows_w = min((int64_t)BN, p.n - n0);
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + m0 * p.lda, (uint32_t)(rows_a * p.lda));
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w + n0 * p.ldw, (uint32_t)(rows_w * p.ldw));
+  __amdgpu_buffer_rsrc_t rw;
+  if constexpr (EPI == EPI_SWIGLU) {
+    // Waves 0-1 load tile rows 0..BN/2-1 = value rows n0.., waves 2-3 load tile
+    // rows BN/2.. = gate rows half_n + n0.. (the resource is based BN/2 rows
+    // earlier, so tile row r maps to half_n + n0 + r - BN/2).
+    static_assert(DMA_A * 8 * 2 == BN / 2, "each wave loads rows of one half");
+    const int64_t rows_h = min((int64_t)(BN / 2), p.half_n - n0);
+    if (wave < 2)
+      rw = make_rsrc(p.w + n0 * p.ldw, (uint32_t)(rows_h * p.ldw));
+    else
+      rw = make_rsrc(p.w + (p.half_n + n0 - BN / 2) * p.ldw, (uint32_t)((BN / 2 + rows_h) * p.ldw));
+  } else {
+    const int64_t rows_w = min((int64_t)BN, p.n - n0);
+    rw = make_rsrc(p.w + n0 * p.ldw, (uint32_t)(rows_w * p.ldw));
+  }
 
   // DMA lane map: 1 KB block b of an operand holds rows 8b..8b+7; lane l fills
   // row 8b + l/8, slot l%8, from logical chunk (l%8) ^ lds_swizzle(row).  The
@@ -398,18 +417,19 @@ __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, 
   constexpr int RD = 2 * (MB + NB);  // ds_read_b128 per K-substep
   static_assert(DMA % QH == 0, "DMA instructions spread evenly over the second half");
 
-  stage_vectors<BM, BN>(p, m0, n0, wave, lane, vec_lds);
-  issue(I0{}, 0);
-  issue(I1{}, 1);
-  wait_vmcnt<DMA, true>();
+  stage_vectors<BM, BN, EPI == EPI_SWIGLU>(p, m0, n0, wave, lane, vec_lds);
+  static_for<NS>([&](auto s) { issue((int)s, (int)s); });
+  wait_vmcnt<(NS - 1) * DMA, true>();
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   read(I0{}, I0{});
-
-  // One stage per iteration; the slot index is a run-time value (unrolling
-  // two stages with constant slots raises register pressure past 256 VGPRs).
+  // The first fragments have landed before the loop: the compiler's wait
+  // tracking then sees the same pending LDS reads on both loop entries and
+  // waits only for the fragments each MFMA needs.
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt/expcnt untouched
+  int j = 0;  // slot of stage kt
   for (int kt = 0; kt < KT; ++kt) {
-    const int j = kt & 1;
+    const int jn = j + 1 == NS ? 0 : j + 1;  // slot of stage kt + 1
     // Substep 0 of stage kt, while reading substep 1 of the same stage.
     mfmas(I0{}, I0{}, std::integral_constant<int, Q>{});
     read(j, I1{});
@@ -418,27 +438,29 @@ __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, 
     // The MFMAs above stay above the wait (they keep the MFMA pipe busy while
     // the wave waits); scheduling barriers pin the order.
     __builtin_amdgcn_sched_barrier(0);
-    // Stage kt+1 has landed for every wave; stage kt is fully read.
-    wait_vmcnt<0, true>();
+    // Stage kt+1 has landed for every wave (the DMAs of stages kt+2 ..
+    // kt+NS-1 may still be in flight); stage kt is fully read.
+    wait_vmcnt<(NS - 2) * DMA, true>();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     // Second half: each remaining MFMA is followed by DMA / QH of the DMA
     // instructions of stage kt+2 and by the reads of one fragment of stage kt+1
     // (unused after the last stage), so DMA issue and reads overlap the MFMA pipe.
-    const Dma d = dma_setup(j, kt + 2);
+    const Dma d = dma_setup(j, kt + NS);
     static_for<QH>([&](auto i) {
       constexpr int q = QH + i, nb = q / MB, mb = q % MB;
       acc[nb][mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
           F[1][MB + nb], F[1][mb], acc[nb][mb], 0, 0, 0, 0, 0, 0);
       static_for<DMA / QH>([&](auto t) { dma_one(d, std::integral_constant<int, i * (DMA / QH) + t>{}); });
-      if constexpr (i < MB + NB) read_one(1 - j, I0{}, i);
+      if constexpr (i < MB + NB) read_one(jn, I0{}, i);
       __builtin_amdgcn_sched_barrier(0);
     });
     // Fragments not covered above (smaller tiles have fewer MFMAs than fragments).
     static_for<(MB + NB > QH ? MB + NB - QH : 0)>([&](auto i) {
-      read_one(1 - j, I0{}, std::integral_constant<int, QH + i>{});
+      read_one(jn, I0{}, std::integral_constant<int, QH + i>{});
     });
+    j = jn;
   }
   wait_vmcnt<0, true>();  // every DMA has landed before the ring is reused
   __builtin_amdgcn_s_barrier();
@@ -451,7 +473,9 @@ __global__ void __launch_bounds__(256) fp8_gemm_pipe2(const GemmParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t ring[PIPE2_LDS];
   __shared__ __attribute__((aligned(1024))) uint8_t vec[VEC_LDS];
   int tm, tn;
-  tile_coords((int)((p.m + 255) / 256), (int)((p.n + 255) / 256), p.group_m, tm, tn);
+  // SwiGLU tiles cover 128 value columns and their 128 gate columns.
+  const int64_t tile_cols = EPI == EPI_SWIGLU ? (p.half_n + 127) / 128 : (p.n + 255) / 256;
+  tile_coords((int)((p.m + 255) / 256), (int)tile_cols, p.group_m, tm, tn);
   pipe2_tile<EPI>(p, tm, tn, ring, __builtin_amdgcn_readfirstlane(lds_addr(ring)), vec,
                   __builtin_amdgcn_readfirstlane(lds_addr(vec)),
                   __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6));
@@ -460,15 +484,15 @@ __global__ void __launch_bounds__(256) fp8_gemm_pipe2(const GemmParams p) {
 // 128 x 128 form for shapes with too few 256 x 256 tiles to fill the GPU: the
 // same pipeline with 64 x 64 per wave (64 accumulator registers), so that two
 // workgroups share a CU and each hides the other's DMA latency and epilogue.
-template <int EPI>
-__global__ void __launch_bounds__(256, 2) fp8_gemm_pipe2s(const GemmParams p) {
-  __shared__ __attribute__((aligned(1024))) uint8_t ring[pipe2_lds(128)];
+template <int EPI, int NS>
+__global__ void __launch_bounds__(256, NS == 2 ? 2 : 1) fp8_gemm_pipe2s(const GemmParams p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[pipe2_lds(128, NS)];
   __shared__ __attribute__((aligned(1024))) uint8_t vec[VEC_LDS];
   int tm, tn;
   tile_coords((int)((p.m + 127) / 128), (int)((p.n + 127) / 128), p.group_m, tm, tn);
-  pipe2_tile<EPI, 128>(p, tm, tn, ring, __builtin_amdgcn_readfirstlane(lds_addr(ring)), vec,
-                       __builtin_amdgcn_readfirstlane(lds_addr(vec)),
-                       __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6));
+  pipe2_tile<EPI, 128, NS>(p, tm, tn, ring, __builtin_amdgcn_readfirstlane(lds_addr(ring)), vec,
+                           __builtin_amdgcn_readfirstlane(lds_addr(vec)),
+                           __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6));
 }
 
 // Persistent form: one workgroup per CU walks its share of the tiles, so the
@@ -511,15 +535,16 @@ __global__ void __launch_bounds__(256) fp8_gemm_persist(const GemmParams p) {
 
 template <int EPI>
 static hipError_t launch_pipe2(const GemmParams& p, hipStream_t s) {
-  const int64_t tiles = ((p.m + 255) / 256) * ((p.n + 255) / 256);
+  const int64_t tile_cols = EPI == EPI_SWIGLU ? (p.half_n + 127) / 128 : (p.n + 255) / 256;
+  const int64_t tiles = ((p.m + 255) / 256) * tile_cols;
   fp8_gemm_pipe2<EPI><<<dim3((unsigned)tiles), dim3(256), 0, s>>>(p);
   return hipGetLastError();
 }
 
-template <int EPI>
+template <int EPI, int NS>
 static hipError_t launch_pipe2s(const GemmParams& p, hipStream_t s) {
   const int64_t tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128);
-  fp8_gemm_pipe2s<EPI><<<dim3((unsigned)tiles), dim3(256), 0, s>>>(p);
+  fp8_gemm_pipe2s<EPI, NS><<<dim3((unsigned)tiles), dim3(256), 0, s>>>(p);
   return hipGetLastError();
 }
 
@@ -554,7 +579,8 @@ static hipError_t launch_cfg(const GemmParams& p, hipStream_t s) {
 // 7 = 256x256 (2x4: two waves per SIMD), 8 = 256x256 pipelined (2x2),
 // 9 = 256x256 pipelined (2x4), 10 = 256x256 two-slot pipelined, 128-byte stages,
 // 11 = tile 10 as a persistent kernel (one workgroup per CU),
-// 12 = 128x128 two-slot pipelined (2x2 waves of 64x64, two workgroups per CU).
+// 12 = 128x128 two-slot pipelined (2x2 waves of 64x64, two workgroups per CU),
+// 13 / 14 = 128x128 with four / three stage slots (one workgroup per CU).
 int pick_tile(const GemmParams& p) {
   auto tiles = [&](int bm, int bn) { return ((p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn); };
   if (tiles(256, 256) >= 512) return 10;
@@ -578,7 +604,9 @@ hipError_t launch_epi(const GemmParams& p, int tile, hipStream_t s) {
     case 9: return launch_pipe<2, 4, EPI>(p, s);
     case 10: return launch_pipe2<EPI>(p, s);
     case 11: return launch_persist<EPI>(p, s);
-    case 12: return launch_pipe2s<EPI>(p, s);
+    case 12: return launch_pipe2s<EPI, 2>(p, s);
+    case 13: return launch_pipe2s<EPI, 4>(p, s);
+    case 14: return launch_pipe2s<EPI, 3>(p, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -604,6 +632,7 @@ hipError_t launch_fp8_gemm(const GemmParams& p, int epi, hipStream_t s) {
     case EPI_GELU: return launch_epi<EPI_GELU>(p, tile, s);
     case EPI_GATE: return launch_epi<EPI_GATE>(p, tile, s);
     case EPI_LORA: return launch_epi<EPI_LORA>(p, tile, s);
+    case EPI_SWIGLU: return launch_pipe2<EPI_SWIGLU>(p, s);  // one tiling: 128 + 128 columns
     default: return hipErrorInvalidValue;
   }
 }

@@ -52,10 +52,30 @@ constexpr int VEC_LDS = 3 * 1024;
 // buffer-load-to-LDS DMA, one instruction each on waves 0, 1 and 2.  Issued
 // with the tile's first K stage, so the caller's first DMA wait and barrier
 // also cover these; entries past the matrix edge read as zero.
-template <int BM, int BN>
+// SWIGLU: tile columns [0, BN/2) are value columns n0.. and [BN/2, BN) the
+// matching gate columns half_n + n0.. (as the GEMM tile maps them).
+template <int BM, int BN, bool SWIGLU = false>
 __device__ __forceinline__ void stage_vectors(const GemmParams& p, int64_t m0, int64_t n0,
                                               int wave, int lane, uint32_t vec_lds) {
   static_assert(BM * 4 <= 1024 && BN * 4 <= 1024, "vector slots hold 256 entries");
+  if constexpr (SWIGLU) {
+    static_assert(BN == 256, "SwiGLU tiles pair 128 value and 128 gate columns");
+    const int half = lane >> 5, l = lane & 31;
+    if (wave == 0) {
+      // Lane l of half h: scales of tile columns 128 h + 4 l .. +3.
+      const int64_t col = (half ? p.half_n : 0) + n0 + 4 * l;
+      lds_dma16(make_rsrc(p.sw, (uint32_t)(p.n * 4)), vec_lds, (uint32_t)(col * 4));
+    } else if (wave == 1) {
+      lds_dma16(make_rsrc(p.sa + m0, (uint32_t)(min((int64_t)BM, p.m - m0) * 4)),
+                vec_lds + 1024, (uint32_t)lane * 16);
+    } else if (wave == 2 && p.bias) {
+      // Lanes 0-15: bias of value columns n0 + 8 l; lanes 16-31: gate columns.
+      const int64_t col = (lane >= 16 ? p.half_n + n0 + 8 * (lane - 16) : n0 + 8 * lane);
+      const uint32_t off = lane < 32 ? (uint32_t)(col * 2) : VFA_OOB;
+      lds_dma16(make_rsrc(p.bias, (uint32_t)(p.n * 2)), vec_lds + 2048, off);
+    }
+    return;
+  }
   if (wave == 0) {
     const uint32_t bytes = p.sw_step ? (uint32_t)(min((int64_t)BN, p.n - n0) * 4) : 4u;
     lds_dma16(make_rsrc(p.sw + (p.sw_step ? n0 : 0), bytes), vec_lds, (uint32_t)lane * 16);
@@ -193,6 +213,50 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
     });
   }
   __syncthreads();
+
+  if constexpr (EPI == EPI_SWIGLU) {
+    // Phase 2 of the SwiGLU tile: value chunk c and gate chunk c + CH/2 of a
+    // row give 8 outputs h = bf16(value * bf16(silu(gate))) (the eager bf16
+    // order of h3_fused_ops.py:184-224); the 16 threads of a row also reduce
+    // max |h| over the tile's 128 output columns for the requantization.
+    constexpr int CHO = CH / 2;   // output chunks per row
+    constexpr int RPO = NT / CHO; // rows per pass
+    static_assert(CHO == 16 && BM % RPO == 0, "one 16-lane group per row");
+    const int c = tid % CHO, r0 = tid / CHO;
+    const int64_t n = n0 + c * 8;
+    const int rows = (int)min((int64_t)BM, p.m - m0);
+    const int parts = (int)((p.half_n + BN / 2 - 1) / (BN / 2));
+    const int part = (int)(n0 / (BN / 2));
+    const float nlog2e = -1.4426950408889634f;
+#pragma unroll 4
+    for (int it = 0; it < BM / RPO; ++it) {
+      const int row = r0 + it * RPO;
+      const bool valid = row < rows;
+      const int rs = row % CH;
+      const v4i vv = *reinterpret_cast<const v4i*>(stage + row * PITCH + ((c ^ rs) << 4));
+      const v4i gg = *reinterpret_cast<const v4i*>(stage + row * PITCH + (((c + CHO) ^ rs) << 4));
+      v4i h;
+      float amax = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t vw = (uint32_t)vv[j], gw = (uint32_t)gg[j];
+        const float g0 = bf16_lo(gw), g1 = bf16_hi(gw);
+        const uint32_t sp = pack_bf16x2(g0 * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g0 * nlog2e)),
+                                        g1 * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g1 * nlog2e)));
+        const uint32_t hw = pack_bf16x2(bf16_lo(vw) * bf16_lo(sp), bf16_hi(vw) * bf16_hi(sp));
+        amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(hw)), fabsf(bf16_hi(hw))));
+        h[j] = (int)hw;
+      }
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+      if (valid) {
+        const int64_t m = m0 + row;
+        if (n < p.half_n) *reinterpret_cast<v4i*>(p.out + m * p.ldo + n) = h;
+        if (c == 0) p.amax_part[m * parts + part] = amax;
+      }
+    }
+    return;
+  }
 
   // Phase 2: LDS rows -> global.  Thread tid owns the 16-byte column chunk
   // c = tid % CH of rows tid / CH + RPP * it, so its column, plane and

@@ -4,7 +4,7 @@
 
 namespace vfa {
 
-enum { EPI_BIAS = 0, EPI_GELU = 1, EPI_GATE = 2, EPI_LORA = 3 };
+enum { EPI_BIAS = 0, EPI_GELU = 1, EPI_GATE = 2, EPI_LORA = 3, EPI_SWIGLU = 4 };
 
 struct GemmParams {
   const uint8_t* a;  // activation codes [m, k], row stride lda bytes
@@ -30,6 +30,7 @@ struct GemmParams {
   int64_t ldb;
   int rank;
   float lora_scale, lora_strength;
+  int64_t half_n;  // EPI_SWIGLU: columns [0, half_n) are values, [half_n, n) gates
   int group_m;  // tile-order group height
   int tile;     // tile configuration (0 = automatic)
 };

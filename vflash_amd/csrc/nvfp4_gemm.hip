@@ -361,6 +361,8 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   read_raw(r0, 0, I0{});
+  // Same pending LDS reads on both loop entries (see the W8A8 kernel).
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
   for (int kt = 0; kt < KT; ++kt) {
     const int j = kt & 1;
     read_raw(r1, j, I1{});

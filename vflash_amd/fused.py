@@ -128,15 +128,27 @@ def fp8_ffn(
     down_bias,
     gate,
     residual,
+    *,
+    activation: str = "gelu_tanh",
 ):
-    """residual + gate * down(requant(gelu_tanh(up(value)))) with reference rounding.
+    """residual + gate * down(requant(act(up(value)))) with reference rounding.
 
     ``value`` and ``residual`` are ``[.., hidden]``; ``gate`` is ``[hidden]``
     (broadcast over tokens) or ``[tokens, hidden]`` with any strides.
+    ``activation`` is ``"gelu_tanh"`` (up projection ``[F, hidden]``) or
+    ``"swiglu"``, the H3 feed-forward (h3_native_denoiser.py:369-382, 563-576):
+    the up projection is the packed ``[2F, hidden]`` value/gate matrix and the
+    activation is ``value * silu(gate)`` with the eager bf16 rounding of
+    h3_fused_ops.py:184-224.
     """
+    if activation not in ("gelu_tanh", "swiglu"):
+        raise ValueError("unknown FFN activation")
     _check_w8a8(execution, value, up_weight, up_scale, up_bias)
     hidden = up_weight.shape[1]
-    if down_weight.shape[1] != up_weight.shape[0] or down_weight.shape[0] != hidden:
+    inner = up_weight.shape[0] // (2 if activation == "swiglu" else 1)
+    if activation == "swiglu" and up_weight.shape[0] % 256:
+        raise ValueError("SwiGLU projections need 2F rows with F a multiple of 128")
+    if down_weight.shape[1] != inner or down_weight.shape[0] != hidden:
         raise ValueError("FFN up/down projections do not chain")
     shape = value.shape
     matrix = value.reshape(-1, hidden)
@@ -148,8 +160,9 @@ def fp8_ffn(
         execution.observer()
     execution.calls["w8a8"] += 2
     codes, act_scale = _quantize(execution, matrix)
+    up = kernels.fp8_gemm_swiglu if activation == "swiglu" else kernels.fp8_gemm_gelu
     with execution.measure("linear.fp8_gemm"):
-        g, amax = kernels.fp8_gemm_gelu(codes, act_scale, up_weight, up_scale, rows, up_bias)
+        g, amax = up(codes, act_scale, up_weight, up_scale, rows, up_bias)
     with execution.measure("linear.activation_quantize"):
         h_codes, h_scale = kernels.requant_rows(g, amax)
     with execution.measure("linear.fp8_gemm"):
@@ -160,13 +173,16 @@ def fp8_ffn(
 
 
 class FP8FeedForward(torch.nn.Module):
-    """FFN block of two row-FP8 projections with a GELU-tanh activation."""
+    """FFN block of two row-FP8 projections with a GELU-tanh or SwiGLU activation."""
 
-    def __init__(self, up, down):
+    def __init__(self, up, down, activation: str = "gelu_tanh"):
         super().__init__()
         if up.execution is not down.execution:
             raise ValueError("FFN projections must share one execution")
+        if activation not in ("gelu_tanh", "swiglu"):
+            raise ValueError("unknown FFN activation")
         self.up, self.down, self.execution = up, down, up.execution
+        self.activation = activation
 
     def forward(self, value, gate, residual):
         return fp8_ffn(
@@ -180,6 +196,7 @@ class FP8FeedForward(torch.nn.Module):
             self.down.bias,
             gate,
             residual,
+            activation=self.activation,
         )
 
 

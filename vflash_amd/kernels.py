@@ -113,6 +113,27 @@ def fp8_gemm_gelu(codes, act_scale, weight, w_scale, rows, bias=None):
     return g, amax
 
 
+def swiglu_parts(n: int) -> int:
+    return int(_lib.library().vflash_swiglu_parts(n))
+
+
+def fp8_gemm_swiglu(codes, act_scale, weight, w_scale, rows, bias=None):
+    """h = bf16(value * bf16(silu(gate))) of the packed projection ``weight``
+    ([2F, K]: value rows, then gate rows), plus per-row |h| maxima per
+    128-column group."""
+    device = _gemm_operands(codes, act_scale, weight, w_scale, rows, bias)
+    n, k = weight.shape
+    if n % 256:
+        raise ValueError("SwiGLU projections need 2F rows with F a multiple of 128")
+    h = torch.empty((rows, n // 2), device=device, dtype=torch.bfloat16)
+    amax = torch.empty((rows, swiglu_parts(n)), device=device, dtype=torch.float32)
+    if rows:
+        call("vflash_fp8_linear_swiglu", ptr(codes), ptr(act_scale), codes.stride(0), ptr(weight),
+             ptr(w_scale), weight.stride(0), rows, n, k, ptr(bias), ptr(h), h.stride(0),
+             ptr(amax), stream_of(device))
+    return h, amax
+
+
 def requant_rows(g, amax_part, pad_to: int = 16):
     """E4M3 codes/scales of ``g`` using its epilogue row maxima."""
     if g.dtype != torch.bfloat16 or g.ndim != 2 or g.stride(1) != 1:
