@@ -11,7 +11,7 @@ HBM.  A step is one ``linear`` call; K timed steps are bracketed by
 events recorded on the launch stream around each of its launches in the timed
 region.  Prints one JSON line.
 
-Other workloads (``qkv``, ``ffn``, ``skinny``, ``nvfp4``, ``small``) print the
+Other workloads (``qkv``, ``ffn``, ``ffn_swiglu``, ``skinny``, ``nvfp4``, ``small``) print the
 same kind of line for the other shapes of this path; ``copy`` times a plain
 1 GiB device copy, the calibration kernel for the HBM byte counters.  For the
 launch-bound shapes (``small``, ``skinny``) the line adds a device-side time
@@ -42,7 +42,7 @@ def parse():
     p.add_argument(
         "--workload",
         default="fp8_linear",
-        choices=["fp8_linear", "qkv", "ffn", "skinny", "nvfp4", "small", "copy"],
+        choices=["fp8_linear", "qkv", "ffn", "ffn_swiglu", "skinny", "nvfp4", "small", "copy"],
     )
     p.add_argument("--skinny-m", type=int, default=1024)
     p.add_argument("--skinny-n", type=int, default=6144)
@@ -223,15 +223,18 @@ def make_workload(args, dev):
         return Workload(wl, metric, "TFLOP/s", flops, step, "fp8_gemm", flops, "mfma",
                         FP8_PEAK_TFLOPS, config, cpu=cpu, launch_bound=wl == "small")
 
-    if wl == "ffn":
+    if wl in ("ffn", "ffn_swiglu"):
         from vflash_amd.fused import fp8_ffn
         from vflash_amd.prepare import quantize_weight_rows
 
-        m, h, f = 32760, 5120, 13824
+        swiglu = wl == "ffn_swiglu"
+        # GELU-tanh FFN at 5120 -> 13824; the H3 SwiGLU FFN at 5376 -> 2 x 14336.
+        m, h, f = (32760, 5376, 14336) if swiglu else (32760, 5120, 13824)
+        up_rows = 2 * f if swiglu else f
         g = torch.Generator().manual_seed(0)
         x = torch.randn((m, h), generator=g).to(torch.bfloat16)
-        wu = torch.randn((f, h), generator=g) * 0.02
-        bu = (torch.randn(f, generator=g) * 0.01).to(torch.bfloat16)
+        wu = torch.randn((up_rows, h), generator=g) * 0.02
+        bu = (torch.randn(up_rows, generator=g) * 0.01).to(torch.bfloat16)
         wdn = torch.randn((h, f), generator=g) * 0.02
         bdn = (torch.randn(h, generator=g) * 0.01).to(torch.bfloat16)
         gate = torch.rand(h, generator=g).to(torch.bfloat16)
@@ -240,20 +243,22 @@ def make_workload(args, dev):
         cdn, sdn = quantize_weight_rows(wdn)
         t = [v.to(dev) for v in (x, cu, su, bu, cdn, sdn, bdn, gate, res)]
         ex = RowFP8Execution("w8a8", activation_quantizer="hip")
-        fp8_ffn(ex, t[0][:64], t[1], t[2], t[3], t[4], t[5], t[6], t[7], t[8][:64])
+        act = "swiglu" if swiglu else "gelu_tanh"
+        fp8_ffn(ex, t[0][:64], t[1], t[2], t[3], t[4], t[5], t[6], t[7], t[8][:64], activation=act)
+        up_kernel = kernels.fp8_gemm_swiglu if swiglu else kernels.fp8_gemm_gelu
 
         def step(i, timer):
             a, sa = kernels.quantize_rows(t[0])
             if timer:
                 timer.start()
-            gg, amax = kernels.fp8_gemm_gelu(a, sa, t[1], t[2], m, t[3])
+            gg, amax = up_kernel(a, sa, t[1], t[2], m, t[3])
             if timer:
                 timer.stop()
             hc, hs = kernels.requant_rows(gg, amax)
             kernels.fp8_gemm_gate_residual(hc, hs, t[4], t[5], m, t[7], t[8], t[6])
 
         cpu = None
-        if not args.no_cpu_baseline:
+        if not args.no_cpu_baseline and not swiglu:
             from oracle.baseline import gelu_ffn
 
             def cpu():
@@ -267,6 +272,13 @@ def make_workload(args, dev):
                         "sample": (f"weight-only FFN chain (dequantized bf16 weights, GELU-tanh, "
                                    f"gate-residual) on {rows} of {m} rows, one call after a warm-up")}
 
+        if swiglu:
+            return Workload(
+                wl, "H3 SwiGLU FP8 FFN TFLOP/s (M=32760, 5376 -> 2x14336 SwiGLU -> 5376, gate-residual)",
+                "TFLOP/s", 2.0 * m * h * up_rows + 2.0 * m * f * h, step, "fp8_gemm_swiglu",
+                2.0 * m * h * up_rows, "mfma", FP8_PEAK_TFLOPS,
+                {"workload": "fp8_ffn_swiglu_m32760_h5376_f14336", "m": m, "hidden": h, "ffn": f,
+                 "step": "quant, packed up GEMM + SwiGLU + row amax, requant, down GEMM + gate-residual"})
         return Workload(
             wl, "Fused FP8 FFN TFLOP/s (M=32760, 5120 -> 13824 GELU-tanh -> 5120, gate-residual)",
             "TFLOP/s", 4.0 * m * h * f, step, "fp8_gemm_gelu", 2.0 * m * h * f, "mfma", FP8_PEAK_TFLOPS,
@@ -290,20 +302,26 @@ def make_workload(args, dev):
         ex = RowFP8Execution("w8a8", activation_quantizer="hip")
         fp8_linear_lora(ex, *sets[0])
 
+        fused_pass = kernels.quantize_lora_supported(k, r)
+
         def step(i, timer):
             xd, cd, sd, bd, ad, bbd = sets[i % len(sets)]
-            a, sa = kernels.quantize_rows(xd)
-            tt = kernels.lora_down(xd, ad)
+            # The launches of fused.fp8_linear_lora: one pass for codes, scales and t.
+            if fused_pass:
+                a, sa, tt = kernels.quantize_rows_lora(xd, ad)
+            else:
+                a, sa = kernels.quantize_rows(xd)
+                tt = kernels.lora_down(xd, ad)
             if timer:
                 timer.start()
             kernels.fp8_gemm_lora(a, sa, cd, sd, m, tt, bbd, bias=bd)
             if timer:
                 timer.stop()
 
-        # Algorithmic HBM bytes of the whole step: x read by the quant and LoRA-down
-        # kernels (bf16), codes written and read back (e4m3), row scales, weights
-        # (e4m3 + fp32 scale + bf16 bias), LoRA A and B, t written and read, bf16 out.
-        step_bytes = (2 * m * k * 2 + 2 * m * k + 8 * m + n * k + 6 * n
+        # Algorithmic HBM bytes of the whole step: x read once (bf16), codes written
+        # and read back (e4m3), row scales, weights (e4m3 + fp32 scale + bf16 bias),
+        # LoRA A and B, t written and read, bf16 out.
+        step_bytes = (2 * m * k + 2 * m * k + 8 * m + n * k + 6 * n
                       + 2 * r * (k + n) + 4 * m * r + 2 * m * n)
         gemm_bytes = m * k + 4 * m + n * k + 6 * n + 2 * m * r + 2 * n * r + 2 * m * n
         return Workload(

@@ -154,6 +154,21 @@ int vflash_lora_down(const void* x, int64_t m, int64_t k, int64_t ldx, const voi
                      int64_t rank, void* t, void* stream);
 
 /*
+ * Per-token E4M3 quantization and the LoRA down-projection of the same rows in
+ * one pass, reading x once: the codes and scales of vflash_quantize_rows_e4m3
+ * bit for bit, and t = bf16(x . A^T) summed in binary32 in another order than
+ * vflash_lora_down (so t may differ from it in the last bf16 place).  Replaces
+ * quantize_activation (src/vflash/native/h3_fp8_activation.py:12-55) plus the
+ * adapter hook's inner F.linear (src/vflash/adapters/h3_reference_lora.py:80-82)
+ * for the skinny adapter linears.
+ *   Requires k % 16 == 0, k <= 2048, rank in {16, 32, 64}, rank * k <= 65536,
+ *   ldx % 8 == 0; x, lora_a 16-byte aligned; codes, t 8-byte aligned.
+ */
+int vflash_quantize_rows_lora_e4m3(const void* x, int64_t m, int64_t k, int64_t ldx,
+                                   void* codes, float* scales, int64_t m_pad,
+                                   const void* lora_a, int64_t rank, void* t, void* stream);
+
+/*
  * W8A8 linear with a fused LoRA up-projection and merge.
  * Replaces the outer F.linear and merge of the adapter hook
  *   (src/vflash/adapters/h3_reference_lora.py:80-90):
@@ -191,9 +206,12 @@ int vflash_nvfp4_linear(const void* a, const float* sa, int64_t lda, const void*
  * (0 = automatic, 1 = 256x256, 2 = 128x128, 3 = 64x64, 4 = 128x256, 5 = 256x128,
  * 6 = 256x256 with 8 waves 4x2, 7 = 256x256 with 8 waves 2x4,
  * 8 / 9 = 256x256 five-stage LDS-DMA ring with 4 / 8 waves,
- * 10 = 256x256 two-slot 128-byte-stage LDS-DMA pipeline (default for large shapes),
+ * 10 = 256x256 two-slot 128-byte-stage LDS-DMA pipeline,
  * 11 = tile 10 as a persistent grid of one workgroup per CU,
- * 12 = 128x128 two-slot pipeline, two workgroups per CU)
+ * 12 = 128x128 two-slot pipeline, two workgroups per CU,
+ * 13 / 14 = 128x128 with four / three stage slots,
+ * 15 = tile 10 with the stage barrier after K-substep 0, 16 = tile 10 with
+ * scalar-offset DMA, 17 = both (default for large shapes))
  * and the tile-order group height (0 = default).  For vflash_nvfp4_linear the
  * values mean 1 = 256x256, 2 = 128x128, 3 = 64x128 (register-staged) and
  * 4 = 256x256 pipelined (default for large shapes); other values select the

@@ -253,6 +253,56 @@ def test_lora_linear_skinny_shapes(dev, m, n, scaling, strength):
     assert torch.equal(off, ex.linear(d(x), d(c), d(s), d(b)))
 
 
+@pytest.mark.parametrize("tile", [2, 3, 10, 12, 17, 18])
+@pytest.mark.parametrize("m,n,k,r", [(300, 640, 512, 32), (129, 384, 1536, 48), (1024, 256, 256, 128)])
+def test_lora_epilogue_under_each_tiling(dev, tile, m, n, k, r):
+    from vflash_amd import _lib
+
+    g = torch.Generator().manual_seed(m + n + k + r)
+    x = torch.randn((m, k), generator=g).to(torch.bfloat16)
+    c, s = quantize_weight_rows(torch.randn((n, k), generator=g) * 0.02)
+    b = (torch.randn(n, generator=g) * 0.01).to(torch.bfloat16)
+    la = (torch.randn((r, k), generator=g) * 0.01).to(torch.bfloat16)
+    lb = (torch.randn((n, r), generator=g) * 0.01).to(torch.bfloat16)
+    d = lambda t: t.to(dev)
+    ex = RowFP8Execution("w8a8", activation_quantizer="triton")
+    _lib.set_gemm_tile(tile)
+    try:
+        out = fp8_linear_lora(ex, d(x), d(c), d(s), d(b), d(la), d(lb), scaling=0.5, strength=1.375)
+    finally:
+        _lib.set_gemm_tile(0)
+    xf = x.float().numpy()
+    base = O.w8a8_linear(xf, u8(c), s.reshape(-1).numpy(), b.float().numpy())
+    delta = O.lora_delta(xf, la.float().numpy(), lb.float().numpy(), 0.5, 1.375)
+    rel_check(out.float().cpu().numpy(), O.lora_merge(base, delta))
+
+
+@pytest.mark.parametrize("m,k,r", [(1, 16, 16), (37, 1536, 32), (1024, 1536, 32), (300, 1024, 64),
+                                   (77, 528, 16), (9, 2048, 32)])
+def test_fused_quantize_and_lora_down_against_the_separate_kernels(dev, m, k, r):
+    g = torch.Generator().manual_seed(m * 7 + k + r)
+    x = (torch.randn((m, k), generator=g) * torch.rand((m, 1), generator=g) * 8).to(torch.bfloat16)
+    if m > 3:
+        x[3] = 0  # a zero row: scale 1, codes 0
+    la = (torch.randn((r, k), generator=g) * 0.01).to(torch.bfloat16)
+    d = lambda t: t.to(dev)
+    codes, scales, t = kernels.quantize_rows_lora(d(x), d(la))
+    ref_codes, ref_scales = kernels.quantize_rows(d(x))
+    assert torch.equal(codes.view(torch.uint8), ref_codes.view(torch.uint8))
+    assert torch.equal(scales, ref_scales)
+    # t: binary32 sums in another order, rounded to bf16 once.  Mostly the same
+    # bits; where the dot product cancels, the two orders differ by a few binary32
+    # ulps of the summands, which the rms term of rel_check covers.
+    t_sep = kernels.lora_down(d(x), d(la)).float().cpu().numpy()
+    t_one = t.float().cpu().numpy()
+    assert (t_one == t_sep).mean() > 0.98
+    rel_check(t_one, t_sep)
+    rel_check(t_one, O.lora_delta(x.float().numpy(), la.float().numpy(), np.eye(r, dtype=np.float32)))
+    # And the codes against the oracle (padding rows included).
+    oc, osc = O.quantize_rows(x.float().numpy())
+    assert np.array_equal(u8(codes), oc) and np.array_equal(scales.reshape(-1).cpu().numpy(), osc)
+
+
 def test_lora_reference_kat_through_the_kernels(dev):
     from tests.conftest import golden
 

@@ -51,6 +51,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
         _I32,
     ),
     "vflash_lora_down": ([_P, _I64, _I64, _I64, _P, _I64, _P, _P], _I32),
+    "vflash_quantize_rows_lora_e4m3": ([_P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P, _P], _I32),
     "vflash_fp8_linear_lora": (
         [_P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _I64, _F32, _F32,
          _P, _I64, _P],

@@ -18,6 +18,8 @@ hipError_t launch_requant_rows(const uint16_t*, int64_t, int64_t, int64_t, const
 hipError_t launch_fp8_gemm(const GemmParams&, int, hipStream_t);
 hipError_t launch_lora_down(const uint16_t*, int64_t, int64_t, int64_t, const uint16_t*, int,
                             uint16_t*, hipStream_t);
+hipError_t launch_quant_lora(const uint16_t*, int64_t, int64_t, int64_t, const uint16_t*, int,
+                             uint16_t*, uint8_t*, float*, int64_t, hipStream_t);
 hipError_t launch_nvfp4(const uint8_t*, const float*, int64_t, const uint8_t*, const uint8_t*,
                         const float*, int64_t, int64_t, int64_t, const uint16_t*, uint16_t*, int64_t, int,
                         int, hipStream_t);
@@ -87,7 +89,7 @@ const char* vflash_status_string(int s) {
 
 int vflash_set_gemm_tile(int tile, int group_m) {
   const int prev = g_tile;
-  if (tile >= 0 && tile <= 14) g_tile = tile;
+  if (tile >= 0 && tile <= 18) g_tile = tile;
   g_group_m = group_m > 0 ? group_m : 8;
   return prev;
 }
@@ -195,6 +197,21 @@ int vflash_lora_down(const void* x, int64_t m, int64_t k, int64_t ldx, const voi
                                       static_cast<const uint16_t*>(lora_a), (int)rank,
                                       static_cast<uint16_t*>(t),
                                       static_cast<hipStream_t>(stream)));
+}
+
+int vflash_quantize_rows_lora_e4m3(const void* x, int64_t m, int64_t k, int64_t ldx,
+                                   void* codes, float* scales, int64_t m_pad,
+                                   const void* lora_a, int64_t rank, void* t, void* stream) {
+  if (!x || !codes || !scales || !lora_a || !t || m < 1 || m_pad < m) return VFLASH_EINVAL;
+  if (k < 16 || k % 16 || k > 2048 || ldx < k || ldx % 8) return VFLASH_EINVAL;
+  if ((rank != 16 && rank != 32 && rank != 64) || rank * k > 65536) return VFLASH_EINVAL;
+  if (!aligned(x, 16) || !aligned(lora_a, 16) || !aligned(t, 8) || !aligned(codes, 8) ||
+      !aligned(scales, 4))
+    return VFLASH_EINVAL;
+  return status(vfa::launch_quant_lora(static_cast<const uint16_t*>(x), m, k, ldx,
+                                       static_cast<const uint16_t*>(lora_a), (int)rank,
+                                       static_cast<uint16_t*>(t), static_cast<uint8_t*>(codes),
+                                       scales, m_pad, static_cast<hipStream_t>(stream)));
 }
 
 int vflash_fp8_linear_lora(const void* a, const float* sa, int64_t lda, const void* w,

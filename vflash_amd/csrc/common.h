@@ -132,6 +132,18 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint32_t lds
                : "m0");
 }
 
+// lds_dma16 with a scalar byte offset added to the lane offset (soffset): the
+// K advance of a stage then costs no vector instruction.  The resource's range
+// check is applied to the lane offset (callers keep lane offset + soffset
+// inside the same buffer row whenever the lane offset is in range).
+__device__ __forceinline__ void lds_dma16_so(__amdgpu_buffer_rsrc_t r, uint32_t lds_dst,
+                                             uint32_t voffset, uint32_t soffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds_dst), "v"(voffset), "s"(r), "s"(soffset)
+               : "m0");
+}
+
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
 // vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8); LGKM selects
 // whether outstanding LDS/scalar operations must also drain.

@@ -299,7 +299,12 @@ constexpr int PIPE2_LDS = pipe2_lds(256);  // two 64 KB stage slots
 
 // NS stage slots: the DMA of stage kt + NS is issued once stage kt is read,
 // so NS - 1 stages are in flight while one is multiplied.
-template <int EPI, int BT = 256, int NS = 2>
+// PRE: MFMAs of K-substep 1 issued before the stage barrier (-1: half of them);
+// the DMA of the next stage is spread over the remaining ones.
+// SDMA: K % 128 == 0; the DMA advances K through the scalar offset and kills
+// stages past the end by switching to an empty buffer resource, so issuing a
+// DMA instruction costs no vector instruction.
+template <int EPI, int BT = 256, int NS = 2, int PRE = -1, bool SDMA = false>
 __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, uint8_t* ring,
                                            uint32_t ring_lds, uint8_t* vec, uint32_t vec_lds,
                                            int wave) {
@@ -376,9 +381,34 @@ __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, 
       lds_dma16(rw, d.base + HALF + w * 1024, off | (w % 2 ? d.kill1 : d.kill0));
     }
   };
+  // Scalar-offset form (SDMA): resources are selected per stage.
+  const __amdgpu_buffer_rsrc_t ra_none = make_rsrc(p.a, 0u), rw_none = make_rsrc(p.w, 0u);
+  struct SDma {
+    __amdgpu_buffer_rsrc_t ra, rw;
+    uint32_t base, kb;
+  };
+  auto sdma_setup = [&](int j, int s) {
+    const bool live = s < KT;
+    return SDma{live ? ra : ra_none, live ? rw : rw_none, wave_lds + j * SLOT,
+                live ? (uint32_t)s * BK : 0u};
+  };
+  auto sdma_one = [&](const SDma& d, auto i) {
+    if constexpr (i < DMA_A) {
+      lds_dma16_so(d.ra, d.base + i * 1024, i % 2 ? a_base1 : a_base0, d.kb + (i / 2) * a_step);
+    } else {
+      constexpr int w = i - DMA_A;
+      lds_dma16_so(d.rw, d.base + HALF + w * 1024, w % 2 ? w_base1 : w_base0,
+                   d.kb + (w / 2) * w_step);
+    }
+  };
   auto issue = [&](int j, int s) {
-    const Dma d = dma_setup(j, s);
-    static_for<DMA>([&](auto i) { dma_one(d, i); });
+    if constexpr (SDMA) {
+      const SDma d = sdma_setup(j, s);
+      static_for<DMA>([&](auto i) { sdma_one(d, i); });
+    } else {
+      const Dma d = dma_setup(j, s);
+      static_for<DMA>([&](auto i) { dma_one(d, i); });
+    }
   };
 
   const int fr = lane & 31, fh = lane >> 5;
@@ -413,10 +443,16 @@ __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, 
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
-  constexpr int Q = MB * NB, QH = Q / 2;
+  constexpr int Q = MB * NB, QB = PRE < 0 ? Q / 2 : PRE, QA = Q - QB;
   constexpr int RD = 2 * (MB + NB);  // ds_read_b128 per K-substep
-  static_assert(DMA % QH == 0, "DMA instructions spread evenly over the second half");
+  static_assert(QA > 0 && DMA % QA == 0, "DMA instructions spread evenly after the barrier");
 
+  // 128x128 LoRA tiles compute their adapter products before the K loop (64
+  // registers); the 256x256 tiles, whose registers hold the main loop, compute
+  // them in the epilogue.
+  constexpr bool LORA_PRE = EPI == EPI_LORA && BT == 128;
+  v16f lora_d[LORA_PRE ? MB * NB : 1];
+  if constexpr (LORA_PRE) lora_blocks<BM, BN, WGM, WGN>(p, m0, n0, wm, wn, lane, lora_d);
   stage_vectors<BM, BN, EPI == EPI_SWIGLU>(p, m0, n0, wave, lane, vec_lds);
   static_for<NS>([&](auto s) { issue((int)s, (int)s); });
   wait_vmcnt<(NS - 1) * DMA, true>();
@@ -434,7 +470,7 @@ __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, 
     mfmas(I0{}, I0{}, std::integral_constant<int, Q>{});
     read(j, I1{});
     interleave(std::integral_constant<int, (RD < Q ? RD : Q)>{});
-    mfmas(I1{}, I0{}, std::integral_constant<int, QH>{});
+    mfmas(I1{}, I0{}, std::integral_constant<int, QB>{});
     // The MFMAs above stay above the wait (they keep the MFMA pipe busy while
     // the wave waits); scheduling barriers pin the order.
     __builtin_amdgcn_sched_barrier(0);
@@ -448,27 +484,35 @@ __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, 
     // instructions of stage kt+2 and by the reads of one fragment of stage kt+1
     // (unused after the last stage), so DMA issue and reads overlap the MFMA pipe.
     const Dma d = dma_setup(j, kt + NS);
-    static_for<QH>([&](auto i) {
-      constexpr int q = QH + i, nb = q / MB, mb = q % MB;
+    const SDma sd = sdma_setup(j, kt + NS);
+    static_for<QA>([&](auto i) {
+      constexpr int q = QB + i, nb = q / MB, mb = q % MB;
       acc[nb][mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
           F[1][MB + nb], F[1][mb], acc[nb][mb], 0, 0, 0, 0, 0, 0);
-      static_for<DMA / QH>([&](auto t) { dma_one(d, std::integral_constant<int, i * (DMA / QH) + t>{}); });
+      static_for<DMA / QA>([&](auto t) {
+        constexpr int di = i * (DMA / QA) + t;
+        if constexpr (SDMA)
+          sdma_one(sd, std::integral_constant<int, di>{});
+        else
+          dma_one(d, std::integral_constant<int, di>{});
+      });
       if constexpr (i < MB + NB) read_one(jn, I0{}, i);
       __builtin_amdgcn_sched_barrier(0);
     });
     // Fragments not covered above (smaller tiles have fewer MFMAs than fragments).
-    static_for<(MB + NB > QH ? MB + NB - QH : 0)>([&](auto i) {
-      read_one(jn, I0{}, std::integral_constant<int, QH + i>{});
+    static_for<(MB + NB > QA ? MB + NB - QA : 0)>([&](auto i) {
+      read_one(jn, I0{}, std::integral_constant<int, QA + i>{});
     });
     j = jn;
   }
   wait_vmcnt<0, true>();  // every DMA has landed before the ring is reused
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  gemm_epilogue<BM, BN, WGM, WGN, EPI, true>(p, acc, m0, n0, wm, wn, tid_v, ring, vec);
+  gemm_epilogue<BM, BN, WGM, WGN, EPI, true>(p, acc, m0, n0, wm, wn, tid_v, ring, vec,
+                                             LORA_PRE ? lora_d : nullptr);
 }
 
-template <int EPI>
+template <int EPI, int PRE = -1, bool SDMA = false>
 __global__ void __launch_bounds__(256) fp8_gemm_pipe2(const GemmParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t ring[PIPE2_LDS];
   __shared__ __attribute__((aligned(1024))) uint8_t vec[VEC_LDS];
@@ -476,21 +520,22 @@ __global__ void __launch_bounds__(256) fp8_gemm_pipe2(const GemmParams p) {
   // SwiGLU tiles cover 128 value columns and their 128 gate columns.
   const int64_t tile_cols = EPI == EPI_SWIGLU ? (p.half_n + 127) / 128 : (p.n + 255) / 256;
   tile_coords((int)((p.m + 255) / 256), (int)tile_cols, p.group_m, tm, tn);
-  pipe2_tile<EPI>(p, tm, tn, ring, __builtin_amdgcn_readfirstlane(lds_addr(ring)), vec,
-                  __builtin_amdgcn_readfirstlane(lds_addr(vec)),
-                  __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6));
+  pipe2_tile<EPI, 256, 2, PRE, SDMA>(p, tm, tn, ring,
+                                     __builtin_amdgcn_readfirstlane(lds_addr(ring)), vec,
+                                     __builtin_amdgcn_readfirstlane(lds_addr(vec)),
+                                     __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6));
 }
 
 // 128 x 128 form for shapes with too few 256 x 256 tiles to fill the GPU: the
 // same pipeline with 64 x 64 per wave (64 accumulator registers), so that two
 // workgroups share a CU and each hides the other's DMA latency and epilogue.
-template <int EPI, int NS>
+template <int EPI, int NS, int PRE = -1, bool SDMA = false>
 __global__ void __launch_bounds__(256, NS == 2 ? 2 : 1) fp8_gemm_pipe2s(const GemmParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t ring[pipe2_lds(128, NS)];
   __shared__ __attribute__((aligned(1024))) uint8_t vec[VEC_LDS];
   int tm, tn;
   tile_coords((int)((p.m + 127) / 128), (int)((p.n + 127) / 128), p.group_m, tm, tn);
-  pipe2_tile<EPI, 128, NS>(p, tm, tn, ring, __builtin_amdgcn_readfirstlane(lds_addr(ring)), vec,
+  pipe2_tile<EPI, 128, NS, PRE, SDMA>(p, tm, tn, ring, __builtin_amdgcn_readfirstlane(lds_addr(ring)), vec,
                            __builtin_amdgcn_readfirstlane(lds_addr(vec)),
                            __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6));
 }
@@ -533,18 +578,18 @@ __global__ void __launch_bounds__(256) fp8_gemm_persist(const GemmParams p) {
   }
 }
 
-template <int EPI>
+template <int EPI, int PRE = -1, bool SDMA = false>
 static hipError_t launch_pipe2(const GemmParams& p, hipStream_t s) {
   const int64_t tile_cols = EPI == EPI_SWIGLU ? (p.half_n + 127) / 128 : (p.n + 255) / 256;
   const int64_t tiles = ((p.m + 255) / 256) * tile_cols;
-  fp8_gemm_pipe2<EPI><<<dim3((unsigned)tiles), dim3(256), 0, s>>>(p);
+  fp8_gemm_pipe2<EPI, PRE, SDMA><<<dim3((unsigned)tiles), dim3(256), 0, s>>>(p);
   return hipGetLastError();
 }
 
-template <int EPI, int NS>
+template <int EPI, int NS, int PRE = -1, bool SDMA = false>
 static hipError_t launch_pipe2s(const GemmParams& p, hipStream_t s) {
   const int64_t tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128);
-  fp8_gemm_pipe2s<EPI, NS><<<dim3((unsigned)tiles), dim3(256), 0, s>>>(p);
+  fp8_gemm_pipe2s<EPI, NS, PRE, SDMA><<<dim3((unsigned)tiles), dim3(256), 0, s>>>(p);
   return hipGetLastError();
 }
 
@@ -583,7 +628,7 @@ static hipError_t launch_cfg(const GemmParams& p, hipStream_t s) {
 // 13 / 14 = 128x128 with four / three stage slots (one workgroup per CU).
 int pick_tile(const GemmParams& p) {
   auto tiles = [&](int bm, int bn) { return ((p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn); };
-  if (tiles(256, 256) >= 512) return 10;
+  if (tiles(256, 256) >= 512) return 17;
   if (tiles(128, 128) >= 256) return 12;
   return 3;
 }
@@ -607,6 +652,15 @@ hipError_t launch_epi(const GemmParams& p, int tile, hipStream_t s) {
     case 12: return launch_pipe2s<EPI, 2>(p, s);
     case 13: return launch_pipe2s<EPI, 4>(p, s);
     case 14: return launch_pipe2s<EPI, 3>(p, s);
+    // Schedules of tile 10: barrier after substep 0 (15), scalar-offset DMA (16),
+    // both (17, the default for large shapes).  The scalar-offset forms need
+    // K % 128 == 0 and fall back to the vector-offset DMA otherwise.
+    case 15: return launch_pipe2<EPI, 0, false>(p, s);
+    case 16: return p.k % 128 ? launch_pipe2<EPI>(p, s) : launch_pipe2<EPI, -1, true>(p, s);
+    case 17: return p.k % 128 ? launch_pipe2<EPI, 0, false>(p, s) : launch_pipe2<EPI, 0, true>(p, s);
+    // Tile 12 with tile 17's schedule.
+    case 18: return p.k % 128 ? launch_pipe2s<EPI, 2, 0, false>(p, s)
+                              : launch_pipe2s<EPI, 2, 0, true>(p, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -632,7 +686,9 @@ hipError_t launch_fp8_gemm(const GemmParams& p, int epi, hipStream_t s) {
     case EPI_GELU: return launch_epi<EPI_GELU>(p, tile, s);
     case EPI_GATE: return launch_epi<EPI_GATE>(p, tile, s);
     case EPI_LORA: return launch_epi<EPI_LORA>(p, tile, s);
-    case EPI_SWIGLU: return launch_pipe2<EPI_SWIGLU>(p, s);  // one tiling: 128 + 128 columns
+    case EPI_SWIGLU:  // one tiling: 128 value + 128 gate columns, tile 17's schedule
+      return p.k % 128 ? launch_pipe2<EPI_SWIGLU, 0, false>(p, s)
+                       : launch_pipe2<EPI_SWIGLU, 0, true>(p, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -44,6 +44,46 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group_
 // Phase 2 (whole workgroup): each thread moves 16-byte row chunks from LDS to
 // global memory with coalesced 16-byte stores, applying the gate-residual
 // epilogue there with coalesced residual loads.
+// LoRA products of one wave's blocks, d[nb * MB + mb] = B[n, :] . t[m, :]
+// (bf16 MFMA, binary32 accumulation), with all loads issued before the MFMAs.
+// Computed ahead of the main loop so the epilogue does not wait on them.
+template <int BM, int BN, int WGM, int WGN>
+__device__ __forceinline__ void lora_blocks(const GemmParams& p, int64_t m0, int64_t n0, int wm,
+                                            int wn, int lane, v16f* d) {
+  constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
+  constexpr int RS = 8;  // rank steps of 16: rank <= 128
+  const int fr = lane & 31, fh = lane >> 5;
+  v8s bf[NB][RS], tf[MB][RS];
+  static_for<NB>([&](auto nb) {
+    const int64_t nrow = n0 + wn * WN + nb * 32 + fr;
+    static_for<RS>([&](auto r) {
+      bf[nb][r] = (r * 16 < p.rank && nrow < p.n)
+                      ? *reinterpret_cast<const v8s*>(p.lora_b + nrow * p.ldb + r * 16 + fh * 8)
+                      : v8s{};
+    });
+  });
+  static_for<MB>([&](auto mb) {
+    const int64_t m = m0 + wm * WM + mb * 32 + fr;
+    static_for<RS>([&](auto r) {
+      tf[mb][r] = (r * 16 < p.rank && m < p.m)
+                      ? *reinterpret_cast<const v8s*>(p.lora_t + m * p.ldt + r * 16 + fh * 8)
+                      : v8s{};
+    });
+  });
+  static_for<NB>([&](auto nb) {
+    static_for<MB>([&](auto mb) {
+      v16f acc = v16f{};
+      static_for<RS>([&](auto r) {
+        if (r * 16 < p.rank)
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, bf[nb][r]),
+                                                        __builtin_bit_cast(v8bf, tf[mb][r]), acc,
+                                                        0, 0, 0);
+      });
+      d[nb * MB + mb] = acc;
+    });
+  });
+}
+
 // LDS bytes of the staged tile vectors: weight scales (or the one scalar),
 // activation row scales, bias.
 constexpr int VEC_LDS = 3 * 1024;
@@ -90,11 +130,14 @@ __device__ __forceinline__ void stage_vectors(const GemmParams& p, int64_t m0, i
 
 // VEC: read the scale and bias vectors from the LDS copy `vec` made by
 // stage_vectors (true), or from global memory (false).
+// lora_d: for EPI_LORA, the per-block LoRA products computed ahead of the main
+// loop ([nb * MB + mb], same layout as acc), or null to compute them here.
 template <int BM, int BN, int WGM, int WGN, int EPI, bool VEC = false>
 __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
                                               v16f (&acc)[BN / WGN / 32][BM / WGM / 32],
                                               int64_t m0, int64_t n0, int wm, int wn, int tid,
-                                              uint8_t* stage, const uint8_t* vec = nullptr) {
+                                              uint8_t* stage, const uint8_t* vec = nullptr,
+                                              const v16f* lora_d = nullptr) {
   constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
   constexpr int NT = 64 * WGM * WGN;
   constexpr int CH = BN / 8;  // 16-byte chunks per staged row
@@ -150,7 +193,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
         const int64_t m = m0 + row;
         const bool mvalid = m < p.m;
         v16f d = v16f{};
-        if constexpr (EPI == EPI_LORA) {
+        if (EPI == EPI_LORA && lora_d) {
+          d = lora_d[nb * MB + mb];
+        } else if constexpr (EPI == EPI_LORA) {
           // delta block = B[n, :] . t[m, :] on bf16 MFMA, binary32 accumulate.
           const int64_t nrow = n0 + wn * WN + nb * 32 + fr;
           const bool nok = nrow < p.n;

@@ -11,44 +11,9 @@
 // The aligned kernel keeps the whole row in VGPRs (16-byte loads, one HBM
 // read per element), reduces the maximum across the wave with XOR shuffles and
 // writes 8 codes per 16-byte input vector.
-#include "common.h"
+#include "quant_ops.h"
 
 namespace vfa {
-
-__device__ __forceinline__ float absmax8(v4i v) {
-  float m = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint32_t w = (uint32_t)v[j];
-    m = fmaxf(m, fabsf(bf16_to_f32(w & 0xffffu)));
-    m = fmaxf(m, fabsf(bf16_to_f32(w >> 16)));
-  }
-  return m;
-}
-
-__device__ __forceinline__ float row_scale(float amax) {
-  return amax > 0.0f ? fmaxf(amax / 448.0f, VFA_FLT_MIN) : 1.0f;
-}
-
-__device__ __forceinline__ uint32_t quant1(float x, float scale) {
-  float q = fminf(fmaxf(x / scale, -448.0f), 448.0f);
-  return f32_to_e4m3(q);
-}
-
-// 8 bf16 values (one 16-byte vector) -> 8 E4M3 codes packed little-endian.
-__device__ __forceinline__ uint2 quant8(v4i v, float scale) {
-  uint32_t c[8];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint32_t w = (uint32_t)v[j];
-    c[2 * j] = quant1(bf16_to_f32(w & 0xffffu), scale);
-    c[2 * j + 1] = quant1(bf16_to_f32(w >> 16), scale);
-  }
-  uint2 r;
-  r.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-  r.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
-  return r;
-}
 
 __device__ __forceinline__ void pad_row(uint8_t* codes, float* scales, int64_t row, int64_t k,
                                         int lane) {

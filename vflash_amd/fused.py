@@ -233,8 +233,19 @@ def fp8_linear_lora(
     rows = matrix.shape[0]
     if matrix.stride(1) != 1 or matrix.stride(0) % 8:
         matrix = matrix.contiguous()
-    codes, act_scale = _quantize(execution, matrix)
-    t = kernels.lora_down(matrix, lora_a)
+    fused_pass = (
+        execution.activation_quantizer != "torch"
+        and kernels.quantize_lora_supported(matrix.shape[1], lora_a.shape[0])
+        and matrix.stride(0) % 8 == 0
+        and lora_a.is_contiguous()
+    )
+    if fused_pass:
+        # One pass over the rows: activation codes/scales and t = bf16(x A^T).
+        with execution.measure("linear.activation_quantize"):
+            codes, act_scale, t = kernels.quantize_rows_lora(matrix, lora_a)
+    else:
+        codes, act_scale = _quantize(execution, matrix)
+        t = kernels.lora_down(matrix, lora_a)
     with execution.measure("linear.fp8_gemm"):
         out = kernels.fp8_gemm_lora(
             codes, act_scale, weight, scale, rows, t, lora_b, scale=scaling, strength=strength,

@@ -198,6 +198,33 @@ def lora_down(x, lora_a):
     return t
 
 
+def quantize_lora_supported(k: int, rank: int) -> bool:
+    """Shapes of the one-pass quantize + LoRA-down kernel."""
+    return k % 16 == 0 and 16 <= k <= 2048 and rank in (16, 32, 64) and rank * k <= 65536
+
+
+def quantize_rows_lora(x, lora_a, pad_to: int = 16):
+    """Codes/scales of ``quantize_rows(x)`` (bit-identical) and ``t = bf16(x lora_a^T)``
+    from one pass over ``x``; see ``quantize_lora_supported`` for the shapes."""
+    if x.dtype != torch.bfloat16 or x.ndim != 2 or x.stride(1) != 1:
+        raise ValueError("LoRA input must be a 2-D BF16 matrix with unit column stride")
+    if lora_a.dtype != torch.bfloat16 or lora_a.ndim != 2 or not lora_a.is_contiguous():
+        raise ValueError("LoRA A must be a contiguous BF16 [rank, K] matrix")
+    device = require_device(x, lora_a)
+    m, k = x.shape
+    rank = lora_a.shape[0]
+    if lora_a.shape[1] != k:
+        raise ValueError("LoRA A does not match the input width")
+    m_pad = (m + pad_to - 1) // pad_to * pad_to
+    codes = torch.empty((m_pad, k), device=device, dtype=E4M3)
+    scales = torch.empty((m_pad, 1), device=device, dtype=torch.float32)
+    t = torch.empty((m, rank), device=device, dtype=torch.bfloat16)
+    if m:
+        call("vflash_quantize_rows_lora_e4m3", ptr(x), m, k, x.stride(0), ptr(codes), ptr(scales),
+             m_pad, ptr(lora_a), rank, ptr(t), stream_of(device))
+    return codes, scales, t
+
+
 def fp8_gemm_lora(codes, act_scale, weight, w_scale, rows, t, lora_b, *, scale=1.0,
                   strength=1.0, bias=None):
     """out = bf16(linear + delta) with delta = bf16(t . lora_b^T) [* scale] [* strength]."""
