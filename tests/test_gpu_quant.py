@@ -136,3 +136,20 @@ def test_row_offsets_beyond_2_pow_31_elements(dev):
     rc, rs = O.quantize_rows(tail.float().numpy(), pad=1)
     assert np.array_equal(c, rc) and np.array_equal(s, rs)
     assert bool((scales[: m - 40] == 1).all())
+
+
+def test_hardware_e4m3_conversion_is_rne_on_every_clamped_binary32(dev):
+    # The quantizers convert with v_cvt_pk_fp8_f32 after clamping to +-448; this
+    # probe compares it with the software RNE encoder (pinned to torch's
+    # float8_e4m3fn cast by the oracle tests) on every binary32 of that range.
+    import subprocess
+    from pathlib import Path
+
+    probe = Path(__file__).resolve().parent / "probes" / "bin" / "e4m3_convert"
+    if not probe.exists():
+        pytest.fail("probe not built: run __graft_entry__.build()")
+    result = subprocess.run([str(probe)], capture_output=True, text=True, timeout=120)
+    assert result.returncode == 0, result.stdout + result.stderr
+    fields = result.stdout.split()
+    assert fields[0] == "values" and int(fields[1]) == 2 * (0x43E00000 + 1)
+    assert fields[2] == "mismatches" and int(fields[3]) == 0, result.stdout
