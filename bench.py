@@ -11,8 +11,8 @@ HBM.  A step is one ``linear`` call; K timed steps are bracketed by
 events recorded on the launch stream around each of its launches in the timed
 region.  Prints one JSON line.
 
-Other workloads (``qkv``, ``ffn``, ``ffn_swiglu``, ``skinny``, ``nvfp4``, ``small``) print the
-same kind of line for the other shapes of this path; ``copy`` times a plain
+Other workloads (``qkv``, ``ffn``, ``ffn_swiglu``, ``skinny``, ``nvfp4``, ``small``,
+``norm_quant``) print the same kind of line for the other shapes of this path; ``copy`` times a plain
 1 GiB device copy, the calibration kernel for the HBM byte counters.  For the
 launch-bound shapes (``small``, ``skinny``) the line adds a device-side time
 per step measured with the launch queue filled ahead.
@@ -42,7 +42,8 @@ def parse():
     p.add_argument(
         "--workload",
         default="fp8_linear",
-        choices=["fp8_linear", "qkv", "ffn", "ffn_swiglu", "skinny", "nvfp4", "small", "copy"],
+        choices=["fp8_linear", "qkv", "ffn", "ffn_swiglu", "skinny", "nvfp4", "small", "norm_quant",
+                 "copy"],
     )
     p.add_argument("--skinny-m", type=int, default=1024)
     p.add_argument("--skinny-n", type=int, default=6144)
@@ -161,6 +162,7 @@ class Workload:
         # Steps shorter than the host's launch cost: the GPU idles between
         # launches, so device time is also measured with the queue filled ahead.
         self.launch_bound = launch_bound
+        self.extra = None  # optional comparison timing: () -> ms per step
 
 
 def rate(work, ms, unit):
@@ -360,6 +362,85 @@ def make_workload(args, dev):
              "mfma": "f16 on exactly dequantized e4m3 activations and e2m1 x e4m3 weights"},
             dtype="e4m3 activations x e2m1 weights (f16 mfma, exact operands)")
 
+    if wl == "norm_quant":
+        from vflash_amd.producers import rmsnorm_modulate_quantize
+
+        # The QKV/FFN-input producer: RMSNorm + adaLN modulation (rows of a
+        # [24, 6, H] table gathered by per-token indices) + per-token E4M3
+        # quantization, one pass over 32760 tokens of hidden 5120.  The indices
+        # (timestep index * 3 + modality tag per token) are constant over runs
+        # of consecutive tokens, as the packed sequence groups tokens by
+        # modality and frame: here 24 runs of equal length in shuffled order.
+        s_tok, h, r = 32760, 5120, 24
+        g = torch.Generator().manual_seed(0)
+        x = torch.randn((1, s_tok, h), generator=g).to(torch.bfloat16)
+        w = (torch.rand(h, generator=g) * 2).to(torch.bfloat16)
+        table = (torch.randn((r, 6, h), generator=g) * 0.5).to(torch.bfloat16)
+        index = torch.randperm(r, generator=g)[torch.arange(s_tok) * r // s_tok]
+        xd, wd, td, idd = x.to(dev), w.to(dev), table.to(dev), index.to(dev)
+        sc, sh = td[:, 1, :], td[:, 0, :]
+        rmsnorm_modulate_quantize(xd[:, :16], wd, sc, sh, eps=1e-6, index=idd[:16])
+
+        def step(i, timer):
+            if timer:
+                timer.start()
+            kernels.rmsnorm_modulate_quantize(xd.view(-1, h), wd, sc, sh, eps=1e-6, index=idd)
+            if timer:
+                timer.stop()
+
+        # Algorithmic HBM bytes: x read once (bf16), codes written (e4m3), fp32 row
+        # scales, the norm weight, the table rows and the indices read once.
+        nbytes = 2.0 * s_tok * h + s_tok * h + 4.0 * s_tok + 2.0 * h + 2.0 * r * 2 * h + 8.0 * s_tok
+
+        def unfused_ms():
+            # The reference's unfused sequence on the same inputs, for comparison:
+            # index_select gathers, F.rms_norm, eager bf16 modulation, HIP quantizer.
+            def chain():
+                scale = sc.index_select(0, idd)
+                shift = sh.index_select(0, idd)
+                n = torch.nn.functional.rms_norm(xd, (h,), wd, 1e-6)
+                kernels.quantize_rows((n * (1.0 + scale) + shift).view(-1, h))
+            for _ in range(3):
+                chain()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(10):
+                chain()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) * 100.0
+
+        cpu = None
+        if not args.no_cpu_baseline:
+            def cpu():
+                from oracle import fp8 as O
+
+                rows = 2048
+                xs = x.view(-1, h)[:rows].float().numpy()
+                idx = index.numpy()[:rows]
+                tf = table.float().numpy()
+                ws = w.float().numpy()
+                times = []
+                for _ in range(3):
+                    t0 = time.perf_counter()
+                    n = O.rms_norm(xs, ws, 1e-6)
+                    O.quantize_rows(O.modulate(n, tf[idx, 1], tf[idx, 0]))
+                    times.append(time.perf_counter() - t0)
+                dt = statistics.median(times)
+                return {"value": nbytes * rows / s_tok / dt / 1e9, "unit": "GB/s", "cores": 1,
+                        "kind": "port",
+                        "sample": (f"numpy restatement of rms_norm + modulation + per-token quantization "
+                                   f"on {rows} of {s_tok} rows, median of 3, {dt * 1e3:.0f} ms")}
+
+        wlo = Workload(
+            wl, "Fused RMSNorm + adaLN modulation + E4M3 quantization GB/s (32760 tokens, hidden 5120)",
+            "GB/s", nbytes, step, "norm_mod_quant_rows", nbytes, "hbm", HBM_PEAK_GBS,
+            {"workload": "norm_mod_quant_m32760_h5120", "m": s_tok, "hidden": h, "table_rows": r,
+             "modulation": "adaLN table rows gathered in place by per-token int64 indices",
+             "index_layout": "24 runs of consecutive tokens"},
+            dtype="bf16 in, e4m3 out", cpu=cpu)
+        wlo.extra = unfused_ms
+        return wlo
+
     if wl == "copy":
         # A plain device copy of 1 GiB: the calibration kernel for the HBM
         # byte counters (FETCH_SIZE / WRITE_SIZE) of the rocprof summaries.
@@ -456,6 +537,8 @@ def main():
         },
         "cpu_baseline": w.cpu() if w.cpu is not None else None,
     }
+    if w.extra is not None:
+        line["unfused_reference_ms_per_step"] = w.extra()
     if device is not None:
         line["device_ms_per_step"] = device
         line["device_rate"] = rate(w.work, device, w.unit)

@@ -117,6 +117,36 @@ int vflash_fp8_linear_swiglu(const void* a, const float* sa, int64_t lda, const 
 int64_t vflash_swiglu_parts(int64_t n);
 
 /*
+ * RMSNorm + adaLN modulation fused with the consuming linear's per-token E4M3
+ * quantization: the producer of the QKV and FFN-input activations.
+ * Replaces _rms_norm + _modulate (src/vflash/native/h3_native_denoiser.py:231-243,
+ *   363-364, called at :535-540 and :565-566) or its fused form
+ *   triton_strict_bf16_modulate (src/vflash/native/h3_fused_ops.py:52-122, 575-611),
+ *   followed by the activation quantization of the next linear
+ *   (src/vflash/native/h3_fp8_activation.py:12-55).
+ *   x       bf16 [m, k] (ldx)
+ *   norm_w  bf16 [k], or NULL (an RMSNorm without weight)
+ *   rstd    = 1 / sqrt(sum_k x^2 / k + eps)                       (binary32)
+ *   y       = bf16(bf16(bf16(x * rstd * norm_w) * bf16(1 + scale)) + shift)
+ *   Modulation rows: x's row r uses t = r % tokens, or index[t] when index is
+ *   not NULL (int64 [tokens], each < mod_rows; the in-place form of the gather
+ *   table[:, j, :].index_select(0, adaln_indices), h3_native_denoiser.py:527-532).
+ *   Row i of scale is scale + i * ld_scale elements, likewise shift.  A row whose
+ *   index is outside [0, mod_rows) gets codes 0 and scale NaN.
+ *   values  optional bf16 [m, k] (ldv) copy of y, for a consumer that needs it.
+ *   codes   e4m3 [m_pad, k] contiguous;  scales fp32 [m_pad]: the arithmetic of
+ *   vflash_quantize_rows_e4m3 applied to y.  Rows m..m_pad-1: codes 0, scale 1.
+ *   Requires k % 8 == 0, k <= 16384, ldx/ld_scale/ld_shift/ldv multiples of 8,
+ *   x, norm_w, scale, shift, values 16-byte aligned, eps finite and >= 0.
+ */
+int vflash_rmsnorm_modulate_quantize_e4m3(const void* x, int64_t m, int64_t k, int64_t ldx,
+                                          const void* norm_w, float eps, const void* scale,
+                                          int64_t ld_scale, const void* shift, int64_t ld_shift,
+                                          int64_t tokens, const int64_t* index, int64_t mod_rows,
+                                          void* values, int64_t ldv, void* codes, float* scales,
+                                          int64_t m_pad, void* stream);
+
+/*
  * Per-token E4M3 requantization from epilogue row maxima.
  * Same arithmetic as vflash_quantize_rows_e4m3 (the down projection's own
  * activation quantization, src/vflash/native/h3_fp8_linear.py:102-108), with

@@ -102,6 +102,32 @@ def silu_mul(packed) -> np.ndarray:
         return bf16_round(value * act)
 
 
+def rms_norm(x, weight, eps: float) -> np.ndarray:
+    """torch.nn.functional.rms_norm of a bf16 [.., H] input with a bf16 weight,
+    as the reference calls it (src/vflash/native/h3_native_denoiser.py:231-243):
+    rstd = 1 / sqrt(sum(x^2) / H + eps) in binary32, n = bf16(x * rstd * w), one
+    rounding; ``weight`` None leaves out the weight.  The sum of squares is
+    formed in binary64 and rounded once to binary32 (any binary32 summation
+    order agrees with it to a few units in the last place).  Pinned against
+    torch's CPU rms_norm: bit-exact where the sum is exact in binary32, within
+    one bf16 step otherwise."""
+    x = np.asarray(x, F32)
+    h = x.shape[-1]
+    ss = F32((x.astype(np.float64) ** 2).sum(-1, keepdims=True))
+    rstd = F32(1.0) / np.sqrt(ss / F32(h) + F32(eps))
+    t = x * rstd
+    return bf16_round(t if weight is None else t * np.asarray(weight, F32))
+
+
+def modulate(n, scale, shift) -> np.ndarray:
+    """adaLN modulation n * (1 + scale) + shift with eager bf16 tensors
+    (h3_native_denoiser.py:363-364; the fused kernel h3_fused_ops.py:52-122 keeps
+    its three roundings): bf16(bf16(n * bf16(1 + scale)) + shift).  Pinned
+    against torch's eager bf16 expression."""
+    one_plus = bf16_round(F32(1.0) + np.asarray(scale, F32))
+    return bf16_round(bf16_round(np.asarray(n, F32) * one_plus) + np.asarray(shift, F32))
+
+
 def gate_residual(residual, gate, y) -> np.ndarray:
     """bf16(residual + bf16(gate * y)) in binary32 (h3_fused_ops.py:153-170)."""
     gated = bf16_round(np.asarray(gate, F32) * np.asarray(y, F32))

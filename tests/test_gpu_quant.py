@@ -153,3 +153,31 @@ def test_hardware_e4m3_conversion_is_rne_on_every_clamped_binary32(dev):
     fields = result.stdout.split()
     assert fields[0] == "values" and int(fields[1]) == 2 * (0x43E00000 + 1)
     assert fields[2] == "mismatches" and int(fields[3]) == 0, result.stdout
+
+
+def fast_division_pairs():
+    """Number of (amax, x) bf16 pairs the row-division probe covers: every
+    positive finite bf16 amax whose scale takes the fast path, with every bf16
+    x (both zeros included) of |x| <= amax."""
+    a = np.arange(1, 0x7F80, dtype=np.uint32)
+    amax = (a << 16).view(np.float32)
+    s = np.maximum(amax / np.float32(448.0), np.float32(1.1754943508222875e-38))
+    fast = (s >= np.float32(2.0**-72)) & (s <= np.finfo(np.float32).max)
+    return int((2 * (a[fast].astype(np.int64) + 1)).sum())
+
+
+def test_fast_row_division_gives_the_ieee_codes_on_every_bf16_pair(dev):
+    # The quantizers divide a row by its scale with Markstein's correction on the
+    # correctly rounded reciprocal; the probe converts both that quotient and the
+    # IEEE one with the hardware E4M3 conversion for every bf16 pair of the fast path.
+    import subprocess
+    from pathlib import Path
+
+    probe = Path(__file__).resolve().parent / "probes" / "bin" / "row_division"
+    if not probe.exists():
+        pytest.fail("probe not built: run __graft_entry__.build()")
+    result = subprocess.run([str(probe)], capture_output=True, text=True, timeout=120)
+    assert result.returncode == 0, result.stdout + result.stderr
+    fields = result.stdout.split()
+    assert fields[0] == "pairs" and int(fields[1]) == fast_division_pairs(), result.stdout
+    assert fields[2] == "code_mismatches" and int(fields[3]) == 0, result.stdout

@@ -162,3 +162,56 @@ def test_merged_qkv_equals_concatenated_projections():
     merged = O.w8a8_linear(x, np.concatenate(ws), np.concatenate(ss))
     parts = [O.w8a8_linear(x, w, s) for w, s in zip(ws, ss)]
     assert np.array_equal(merged, np.concatenate(parts, axis=1))
+
+
+@pytest.mark.parametrize("hidden", [64, 5120, 5376])
+@pytest.mark.parametrize("eps", [0.0, 1e-6, 1e-5, 0.25])
+def test_rms_norm_oracle_is_torch_where_the_sum_is_exact(hidden, eps):
+    # x = k/16 with |k| <= 16: every square is a multiple of 2^-8 and every
+    # partial sum is exact in binary32, so any summation order gives one rstd
+    # and torch's rms_norm must agree bit for bit (with and without weight).
+    g = torch.Generator().manual_seed(hidden)
+    x = (torch.randint(-16, 17, (32, hidden), generator=g).float() / 16).to(torch.bfloat16)
+    w = (torch.rand(hidden, generator=g) * 2).to(torch.bfloat16)
+    ref = torch.nn.functional.rms_norm(x, (hidden,), w, eps).float().numpy()
+    assert np.array_equal(O.rms_norm(x.float().numpy(), w.float().numpy(), eps), ref)
+    ref0 = torch.nn.functional.rms_norm(x, (hidden,), None, eps).float().numpy()
+    assert np.array_equal(O.rms_norm(x.float().numpy(), None, eps), ref0)
+
+
+def test_rms_norm_oracle_keeps_eps_in_binary32_and_rounds_once():
+    # Mean squares near eps: a bf16-rounded eps, or a bf16 rounding before the
+    # weight, changes thousands of outputs; the oracle changes none.
+    g = torch.Generator().manual_seed(1)
+    x = (torch.randint(-16, 17, (64, 512), generator=g).float() * 2.0**-12).to(torch.bfloat16)
+    w = (torch.rand(512, generator=g) * 2).to(torch.bfloat16)
+    ref = torch.nn.functional.rms_norm(x, (512,), w, 1e-5).float().numpy()
+    xs, ws = x.float().numpy(), w.float().numpy()
+    assert np.array_equal(O.rms_norm(xs, ws, 1e-5), ref)
+    bf16_eps = float(torch.tensor(1e-5).to(torch.bfloat16))
+    assert (O.rms_norm(xs, ws, bf16_eps) != ref).sum() > 1000
+    assert (bf16_round(O.rms_norm(xs, None, 1e-5) * ws) != ref).sum() > 1000
+
+
+def test_rms_norm_oracle_tracks_torch_on_random_rows():
+    g = torch.Generator().manual_seed(2)
+    x = (torch.randn(128, 5120, generator=g) * 3).to(torch.bfloat16)
+    w = (torch.rand(5120, generator=g) * 2).to(torch.bfloat16)
+    ref = torch.nn.functional.rms_norm(x, (5120,), w, 1e-6).float().numpy().astype(np.float64)
+    got = O.rms_norm(x.float().numpy(), w.float().numpy(), 1e-6).astype(np.float64)
+    # Summation order only: at most one bf16 step, on a few elements.
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0**-7)
+    assert (got != ref).mean() < 1e-4
+
+
+def test_modulate_oracle_is_torch_eager_bf16():
+    g = torch.Generator().manual_seed(3)
+    n = (torch.randn(64, 512, generator=g) * 4).to(torch.bfloat16)
+    scale = (torch.randn(64, 512, generator=g) * 0.7).to(torch.bfloat16)
+    shift = torch.randn(64, 512, generator=g).to(torch.bfloat16)
+    ref = (n * (1.0 + scale) + shift).float().numpy()
+    got = O.modulate(n.float().numpy(), scale.float().numpy(), shift.float().numpy())
+    assert np.array_equal(got, ref)
+    # Leaving out the bf16 rounding of 1 + scale is visible.
+    fused = bf16_round(bf16_round(n.float().numpy() * (1.0 + scale.float().numpy())) + shift.float().numpy())
+    assert (fused != ref).sum() > 0

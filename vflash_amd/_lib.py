@@ -45,6 +45,11 @@ SIGNATURES: dict[str, tuple[list, object]] = {
         _I32,
     ),
     "vflash_swiglu_parts": ([_I64], _I64),
+    "vflash_rmsnorm_modulate_quantize_e4m3": (
+        [_P, _I64, _I64, _I64, _P, _F32, _P, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _P,
+         _I64, _P],
+        _I32,
+    ),
     "vflash_requant_rows_e4m3": ([_P, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P], _I32),
     "vflash_fp8_linear_gate_residual": (
         [_P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _I64, _P],

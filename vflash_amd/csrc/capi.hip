@@ -13,6 +13,7 @@
 namespace vfa {
 hipError_t launch_quant_rows(const uint16_t*, int64_t, int64_t, int64_t, uint8_t*, float*,
                              int64_t, hipStream_t);
+hipError_t launch_norm_mod_quant(const NormModParams&, hipStream_t);
 hipError_t launch_requant_rows(const uint16_t*, int64_t, int64_t, int64_t, const float*, int,
                                uint8_t*, float*, int64_t, hipStream_t);
 hipError_t launch_fp8_gemm(const GemmParams&, int, hipStream_t);
@@ -155,6 +156,45 @@ int vflash_fp8_linear_swiglu(const void* a, const float* sa, int64_t lda, const 
   p.half_n = n / 2;
   p.amax_part = amax_part;
   return status(vfa::launch_fp8_gemm(p, vfa::EPI_SWIGLU, static_cast<hipStream_t>(stream)));
+}
+
+int vflash_rmsnorm_modulate_quantize_e4m3(const void* x, int64_t m, int64_t k, int64_t ldx,
+                                          const void* norm_w, float eps, const void* scale,
+                                          int64_t ld_scale, const void* shift, int64_t ld_shift,
+                                          int64_t tokens, const int64_t* index, int64_t mod_rows,
+                                          void* values, int64_t ldv, void* codes, float* scales,
+                                          int64_t m_pad, void* stream) {
+  if (!x || !scale || !shift || !codes || !scales) return VFLASH_EINVAL;
+  if (m < 1 || k < 8 || k % 8 || k > 16384 || m_pad < m || m_pad >= (int64_t(1) << 33))
+    return VFLASH_EINVAL;
+  if (ldx < k || ldx % 8 || ld_scale < k || ld_scale % 8 || ld_shift < k || ld_shift % 8)
+    return VFLASH_EINVAL;
+  if (!aligned(x, 16) || !aligned(scale, 16) || !aligned(shift, 16) || !aligned(codes, 8) ||
+      !aligned(scales, 4) || (norm_w && !aligned(norm_w, 16)))
+    return VFLASH_EINVAL;
+  if (!(eps >= 0.0f) || eps > 3.4e38f) return VFLASH_EINVAL;  // rejects NaN and infinity
+  if (tokens < 1 || (index && (mod_rows < 1 || !aligned(index, 8)))) return VFLASH_EINVAL;
+  if (values && (ldv < k || ldv % 8 || !aligned(values, 16))) return VFLASH_EINVAL;
+  vfa::NormModParams p{};
+  p.x = static_cast<const uint16_t*>(x);
+  p.m = m;
+  p.k = k;
+  p.ldx = ldx;
+  p.norm_w = static_cast<const uint16_t*>(norm_w);
+  p.eps = eps;
+  p.scale = static_cast<const uint16_t*>(scale);
+  p.ld_scale = ld_scale;
+  p.shift = static_cast<const uint16_t*>(shift);
+  p.ld_shift = ld_shift;
+  p.tokens = tokens;
+  p.index = index;
+  p.mod_rows = index ? mod_rows : tokens;
+  p.values = static_cast<uint16_t*>(values);
+  p.ldv = ldv;
+  p.codes = static_cast<uint8_t*>(codes);
+  p.scales = scales;
+  p.m_pad = m_pad;
+  return status(vfa::launch_norm_mod_quant(p, static_cast<hipStream_t>(stream)));
 }
 
 int vflash_requant_rows_e4m3(const void* g, int64_t m, int64_t k, int64_t ldg,

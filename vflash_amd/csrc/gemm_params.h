@@ -1,4 +1,5 @@
-// Kernel-side parameter block of the E4M3 GEMM family (not part of the C-ABI).
+// Kernel-side parameter blocks of the E4M3 GEMM family and of the fused
+// norm/modulation quantizer (not part of the C-ABI).
 #pragma once
 #include <stdint.h>
 
@@ -33,6 +34,26 @@ struct GemmParams {
   int64_t half_n;  // EPI_SWIGLU: columns [0, half_n) are values, [half_n, n) gates
   int group_m;  // tile-order group height
   int tile;     // tile configuration (0 = automatic)
+};
+
+// RMSNorm + adaLN modulation + per-token E4M3 quantization (producer.hip).
+struct NormModParams {
+  const uint16_t* x;
+  int64_t m, k, ldx;
+  const uint16_t* norm_w;  // [k], or null for an RMSNorm without weight
+  float eps;
+  const uint16_t* scale;
+  int64_t ld_scale;
+  const uint16_t* shift;
+  int64_t ld_shift;
+  int64_t tokens;
+  const int64_t* index;  // [tokens] modulation rows, or null
+  int64_t mod_rows;      // rows addressable through index
+  uint16_t* values;      // optional bf16 copy of y
+  int64_t ldv;
+  uint8_t* codes;
+  float* scales;
+  int64_t m_pad;
 };
 
 }  // namespace vfa

@@ -192,11 +192,7 @@ __global__ void __launch_bounds__(256) quant_lora_rows(
     static_for<QL_VPL>([&](auto i) { amax = fmaxf(amax, absmax8(v[i])); });
     amax = wave_max(amax);
     const float scale = row_scale(amax);
-    uint2* cr = reinterpret_cast<uint2*>(codes + row * k);
-    static_for<QL_VPL>([&](auto i) {
-      const int j = lane + 64 * i;
-      if (j < nvec) cr[j] = quant8(v[i], scale);
-    });
+    quant_row_regs<QL_VPL>(reinterpret_cast<uint2*>(codes + row * k), v, lane, nvec, scale);
     if (lane == 0) scales[row] = scale;
   }
 }

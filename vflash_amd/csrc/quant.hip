@@ -51,12 +51,7 @@ __global__ void __launch_bounds__(256) quant_rows_vec(const uint16_t* __restrict
   }
   amax = wave_max(amax);
   const float scale = row_scale(amax);
-  uint2* cr = reinterpret_cast<uint2*>(codes + row * k);
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    int j = lane + 64 * i;
-    if (j < nvec) cr[j] = quant8(v[i], scale);
-  }
+  quant_row_regs<VPL>(reinterpret_cast<uint2*>(codes + row * k), v, lane, nvec, scale);
   if (lane == 0) scales[row] = scale;
 }
 
@@ -106,7 +101,12 @@ __global__ void __launch_bounds__(256) requant_rows(const uint16_t* __restrict__
   const v4i* gr = reinterpret_cast<const v4i*>(g + row * ldg);
   uint2* cr = reinterpret_cast<uint2*>(codes + row * k);
   const int nvec = (int)(k >> 3);
-  for (int j = lane; j < nvec; j += 64) cr[j] = quant8(__builtin_nontemporal_load(gr + j), scale);
+  const RowDivisor d = row_divisor(scale);
+  if (d.fast) {
+    for (int j = lane; j < nvec; j += 64) cr[j] = quant8<true>(__builtin_nontemporal_load(gr + j), d);
+  } else {
+    for (int j = lane; j < nvec; j += 64) cr[j] = quant8<false>(__builtin_nontemporal_load(gr + j), d);
+  }
   if (lane == 0) scales[row] = scale;
 }
 

@@ -26,6 +26,7 @@ from typing import Any
 import torch
 
 from vflash_amd import _lib, kernels
+from vflash_amd.producers import QuantizedRows
 
 
 def _quantize_activation_torch(matrix):
@@ -114,6 +115,8 @@ class RowFP8Execution:
         ):
             raise ValueError("FP8 bias differs from the declared output")
         if self.mode == "weight-only":
+            if isinstance(value, QuantizedRows):
+                raise ValueError("pre-quantized activations require the w8a8 mode")
             self.calls["weight_only"] += 1
             restored = (weight.float() * scale).to(value.dtype)
             return torch.nn.functional.linear(value, restored, bias)
@@ -121,13 +124,17 @@ class RowFP8Execution:
             raise ValueError("W8A8 requires gfx950 (MI355X) BF16 inputs")
         self.calls["w8a8"] += 1
         shape = value.shape
-        matrix = value.reshape(-1, shape[-1])
-        rows = matrix.shape[0]
-        if self.activation_quantizer == "torch":
-            codes, act_scale = _quantize_activation_torch(matrix)
+        if isinstance(value, QuantizedRows):
+            # Codes and scales from a fused producer (vflash_amd.producers).
+            codes, act_scale, rows = value.codes, value.scales, value.rows
         else:
-            with self.measure("linear.activation_quantize"):
-                codes, act_scale = kernels.quantize_rows(matrix)
+            matrix = value.reshape(-1, shape[-1])
+            rows = matrix.shape[0]
+            if self.activation_quantizer == "torch":
+                codes, act_scale = _quantize_activation_torch(matrix)
+            else:
+                with self.measure("linear.activation_quantize"):
+                    codes, act_scale = kernels.quantize_rows(matrix)
         with self.measure("linear.fp8_gemm"):
             output = kernels.fp8_gemm(codes, act_scale, weight, scale, rows, bias)
         return output.reshape(*shape[:-1], weight.shape[0])

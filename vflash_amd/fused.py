@@ -14,6 +14,10 @@ of the reference's unfused sequence:
   gate + residual in the epilogue (h3_fused_ops.py:124-170 rounding);
 * LoRA (src/vflash/adapters/h3_reference_lora.py:75-90): ``t = bf16(x A^T)``,
   then the base linear with ``bf16(t B^T)`` merged in its epilogue.
+
+Each also accepts, as ``value``, the ``QuantizedRows`` of a fused producer
+(vflash_amd.producers), whose codes and scales take the place of its own
+activation quantization.
 """
 
 from __future__ import annotations
@@ -22,6 +26,7 @@ import torch
 
 from vflash_amd import kernels
 from vflash_amd.fp8_linear import RowFP8Execution, _quantize_activation_torch, w8a8_supported
+from vflash_amd.producers import QuantizedRows
 
 
 def _quantize(execution: RowFP8Execution, matrix):
@@ -29,6 +34,16 @@ def _quantize(execution: RowFP8Execution, matrix):
         return _quantize_activation_torch(matrix)
     with execution.measure("linear.activation_quantize"):
         return kernels.quantize_rows(matrix)
+
+
+def _activation(execution: RowFP8Execution, value):
+    """(codes, scales, rows) of a bf16 ``[.., K]`` activation, or of the rows a
+    fused producer already quantized (``QuantizedRows``)."""
+    if isinstance(value, QuantizedRows):
+        return value.codes, value.scales, value.rows
+    matrix = value.reshape(-1, value.shape[-1])
+    codes, act_scale = _quantize(execution, matrix)
+    return codes, act_scale, matrix.shape[0]
 
 
 def _check_w8a8(execution: RowFP8Execution, value, weight, scale, bias=None):
@@ -76,9 +91,7 @@ def qkv_linear(execution: RowFP8Execution, value, weight, scale, bias=None, *, p
         execution.observer()
     execution.calls["w8a8"] += 1
     shape = value.shape
-    matrix = value.reshape(-1, shape[-1])
-    rows = matrix.shape[0]
-    codes, act_scale = _quantize(execution, matrix)
+    codes, act_scale, rows = _activation(execution, value)
     inner = weight.shape[0] // 3
     with execution.measure("linear.fp8_gemm"):
         if planes:
@@ -151,15 +164,14 @@ def fp8_ffn(
     if down_weight.shape[1] != inner or down_weight.shape[0] != hidden:
         raise ValueError("FFN up/down projections do not chain")
     shape = value.shape
-    matrix = value.reshape(-1, hidden)
-    rows = matrix.shape[0]
+    rows = shape.numel() // hidden
     res = residual.reshape(-1, down_weight.shape[0])
     if res.shape[0] != rows:
         raise ValueError("residual rows differ from the FFN input rows")
     if execution.observer is not None and sum(execution.calls.values()) % 200 == 0:
         execution.observer()
     execution.calls["w8a8"] += 2
-    codes, act_scale = _quantize(execution, matrix)
+    codes, act_scale, rows = _activation(execution, value)
     up = kernels.fp8_gemm_swiglu if activation == "swiglu" else kernels.fp8_gemm_gelu
     with execution.measure("linear.fp8_gemm"):
         g, amax = up(codes, act_scale, up_weight, up_scale, rows, up_bias)
@@ -229,6 +241,17 @@ def fp8_linear_lora(
         execution.observer()
     execution.calls["w8a8"] += 1
     shape = value.shape
+    if isinstance(value, QuantizedRows):
+        # The producer quantized the rows; the adapter reads the bf16 rows it kept.
+        if value.values is None:
+            raise ValueError("an adapter on pre-quantized rows needs the producer's bf16 values")
+        t = kernels.lora_down(value.values.reshape(-1, shape[-1]), lora_a)
+        with execution.measure("linear.fp8_gemm"):
+            out = kernels.fp8_gemm_lora(
+                value.codes, value.scales, weight, scale, value.rows, t, lora_b, scale=scaling,
+                strength=strength, bias=bias,
+            )
+        return out.reshape(*shape[:-1], weight.shape[0])
     matrix = value.reshape(-1, shape[-1])
     rows = matrix.shape[0]
     if matrix.stride(1) != 1 or matrix.stride(0) % 8:

@@ -44,6 +44,50 @@ def quantize_rows(matrix: torch.Tensor, pad_to: int = 16):
     return codes, scales
 
 
+def rmsnorm_modulate_quantize(matrix, norm_weight, scale, shift, *, eps, index=None,
+                              keep_values=False, pad_to: int = 16):
+    """RMSNorm + adaLN modulation + per-token E4M3 quantization in one pass.
+
+    ``matrix`` is bf16 ``[M, K]`` with unit column stride, ``norm_weight`` bf16
+    ``[K]`` or None.  ``scale`` and ``shift`` are bf16 ``[R, K]`` with unit column
+    stride and any row stride (for instance ``table[:, j, :]`` of a ``[R, 6, K]``
+    adaLN table).  Row r of ``matrix`` uses modulation row ``r % R``, or
+    ``index[r % T]`` for an int64 ``index`` of length T.  Returns codes
+    ``[ceil16(M), K]``, scales ``[ceil16(M), 1]`` and, with ``keep_values``, the
+    modulated bf16 ``[M, K]`` (else None).
+    """
+    if matrix.dtype != torch.bfloat16 or matrix.ndim != 2 or matrix.stride(1) != 1:
+        raise ValueError("the fused norm/modulation needs a 2-D BF16 matrix with unit column stride")
+    m, k = matrix.shape
+    for t in (scale, shift):
+        if t.dtype != torch.bfloat16 or t.ndim != 2 or t.shape[1] != k or t.stride(1) != 1:
+            raise ValueError("modulation rows must be BF16 [R, K] with unit column stride")
+    if scale.shape != shift.shape:
+        raise ValueError("scale and shift must have the same rows")
+    if norm_weight is not None and (
+        norm_weight.dtype != torch.bfloat16 or norm_weight.shape != (k,) or not norm_weight.is_contiguous()
+    ):
+        raise ValueError("the RMSNorm weight must be a contiguous BF16 [K] vector")
+    if index is not None:
+        if index.dtype != torch.int64 or index.ndim != 1 or not index.is_contiguous() or index.numel() < 1:
+            raise ValueError("modulation indices must be a contiguous int64 vector")
+        tokens = index.numel()
+    else:
+        tokens = scale.shape[0]
+    if tokens < 1 or m % tokens:
+        raise ValueError("activation rows must be a whole number of modulated token blocks")
+    device = require_device(matrix, scale, shift, norm_weight, index)
+    m_pad = (m + pad_to - 1) // pad_to * pad_to
+    codes = torch.empty((m_pad, k), device=device, dtype=E4M3)
+    scales = torch.empty((m_pad, 1), device=device, dtype=torch.float32)
+    values = torch.empty((m, k), device=device, dtype=torch.bfloat16) if keep_values else None
+    call("vflash_rmsnorm_modulate_quantize_e4m3", ptr(matrix), m, k, matrix.stride(0),
+         ptr(norm_weight), float(eps), ptr(scale), scale.stride(0), ptr(shift), shift.stride(0),
+         tokens, ptr(index), scale.shape[0], ptr(values), k, ptr(codes), ptr(scales), m_pad,
+         stream_of(device))
+    return codes, scales, values
+
+
 def _gemm_operands(codes, act_scale, weight, w_scale, rows, bias):
     if codes.dtype != E4M3 or weight.dtype != E4M3 or codes.ndim != 2 or weight.ndim != 2:
         raise ValueError("E4M3 GEMM operands must be 2-D float8_e4m3fn matrices")
