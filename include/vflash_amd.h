@@ -161,17 +161,23 @@ int vflash_requant_rows_e4m3(const void* g, int64_t m, int64_t k, int64_t ldg,
 /*
  * FFN down-projection with the adaLN gate-residual epilogue.
  * Replaces RowFP8Execution.linear + triton_strict_bf16_gate_residual
- *   (src/vflash/native/h3_fused_ops.py:124-170, 614-657).
+ *   (src/vflash/native/h3_fused_ops.py:124-170, 614-657), including the gather
+ *   of the gate rows, table[:, j, :].index_select(0, adaln_indices)
+ *   (src/vflash/native/h3_native_denoiser.py:527-532, 556-561), read in place.
  *   y   = bf16(bf16(acc * sa * sw) + bias)
- *   out = bf16(residual[m, n] + bf16(gate[m * gate_ts + n * gate_hs] * y))
- *   gate_ts = 0 broadcasts one gate row over all tokens.  out may alias residual
- *   only when ldo == ldr.
+ *   out = bf16(residual[m, n] + bf16(gate[g * gate_ts + n * gate_hs] * y))
+ *   g   = m % gate_tokens, or gate_index[m % gate_tokens] when gate_index is not
+ *         NULL (int64, each < gate_rows; a row whose index is outside gets NaN).
+ *   gate_ts = 0 broadcasts one gate row over all tokens; gate_tokens = m gives
+ *   one gate row per output row.  out may alias residual only when ldo == ldr.
  */
 int vflash_fp8_linear_gate_residual(const void* a, const float* sa, int64_t lda, const void* w,
                                     const float* sw, int64_t ldw, int64_t m, int64_t n,
                                     int64_t k, const void* bias, const void* gate,
-                                    int64_t gate_ts, int64_t gate_hs, const void* residual,
-                                    int64_t ldr, void* out, int64_t ldo, void* stream);
+                                    int64_t gate_ts, int64_t gate_hs, int64_t gate_tokens,
+                                    const int64_t* gate_index, int64_t gate_rows,
+                                    const void* residual, int64_t ldr, void* out, int64_t ldo,
+                                    void* stream);
 
 /*
  * LoRA down-projection t = bf16(x . A^T) (binary32 accumulation).

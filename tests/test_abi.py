@@ -45,7 +45,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_status_strings_and_version():
     lib = _lib.library()
-    assert lib.vflash_abi_version() == 1
+    assert lib.vflash_abi_version() == 2
     assert lib.vflash_status_string(_lib.VFLASH_EINVAL) == b"argument outside the declared contract"
     assert lib.vflash_row_parts(13824) == 216 and lib.vflash_row_parts(64) == 1
 
@@ -74,3 +74,22 @@ def test_nvfp4_and_lora_contracts():
     assert lib.vflash_nvfp4_linear(p, p, 64, p, p, p, 1, 64, 64, None, p, 64, None) == -1
     # rank not a multiple of 16
     assert lib.vflash_lora_down(p, 4, 64, 64, p, 20, p, None) == -1
+
+
+def test_gate_residual_and_producer_contracts():
+    lib = _lib.library()
+    p = ctypes.c_void_p(256)
+    # gate_tokens 0, and an index without rows: rejected before any launch
+    assert lib.vflash_fp8_linear_gate_residual(p, p, 64, p, p, 64, 16, 64, 64, None, p, 64, 1, 0,
+                                               None, 0, p, 64, p, 64, None) == -1
+    assert lib.vflash_fp8_linear_gate_residual(p, p, 64, p, p, 64, 16, 64, 64, None, p, 64, 1, 16,
+                                               p, 0, p, 64, p, 64, None) == -1
+    # k not a multiple of 8, a NaN eps, a misaligned modulation row stride
+    args = [p, 4, 12, 16, None, 1e-6, p, 16, p, 16, 4, None, 0, None, 0, p, p, 16, None]
+    assert lib.vflash_rmsnorm_modulate_quantize_e4m3(*args) == -1
+    args[2] = 16
+    args[5] = float("nan")
+    assert lib.vflash_rmsnorm_modulate_quantize_e4m3(*args) == -1
+    args[5] = 1e-6
+    args[7] = 20
+    assert lib.vflash_rmsnorm_modulate_quantize_e4m3(*args) == -1

@@ -319,3 +319,54 @@ def test_lora_reference_kat_through_the_kernels(dev):
                           torch.from_numpy(la).to(torch.bfloat16).to(dev))
     tn = t.float().cpu().numpy()
     assert np.array_equal(tn, O.lora_delta(x, la, np.eye(128, dtype=np.float32)))
+
+
+def test_gate_rows_gathered_in_place_and_broadcast_over_the_batch(dev):
+    # gate_msa / gate_mlp = table[:, j, :].index_select(0, adaln_indices), broadcast
+    # over the batch (h3_native_denoiser.py:527-532, 556-561, h3_fused_ops.py:124-170).
+    b, s, h, f, r = 2, 96, 512, 384, 7
+    g = torch.Generator().manual_seed(41)
+    x = torch.randn((b * s, f), generator=g).to(torch.bfloat16)
+    cd, sd = quantize_weight_rows(torch.randn((h, f), generator=g) * 0.02)
+    bd = (torch.randn(h, generator=g) * 0.01).to(torch.bfloat16)
+    res = torch.randn((b * s, h), generator=g).to(torch.bfloat16)
+    table = torch.rand((r, 6, h), generator=g).to(torch.bfloat16).to(dev)
+    index = torch.randint(0, r, (s,), generator=g).to(dev)
+    d = lambda t: t.to(dev)
+    a, sa = kernels.quantize_rows(d(x))
+    gate = table[:, 2, :]
+    gathered = gate.index_select(0, index)
+    run = lambda gt, **kw: kernels.fp8_gemm_gate_residual(a, sa, d(cd), d(sd), b * s, gt, d(res),
+                                                           d(bd), **kw)
+    ref = run(gathered.repeat(b, 1))
+    assert torch.equal(run(gathered), ref)
+    assert torch.equal(run(gate, gate_index=index), ref)
+    # Through the FFN composition, with the producer's rows as input.
+    y = O.gate_residual(res.float().numpy(), gathered.repeat(b, 1).float().cpu().numpy(),
+                        O.w8a8_linear(x.float().numpy(), u8(cd), sd.reshape(-1).numpy(), bd.float().numpy()))
+    rel_check(ref.float().cpu().numpy(), y)
+    # Indices outside the table: NaN rows; every other row unchanged.
+    bad = index.clone()
+    bad[3], bad[10] = r, -2
+    out = run(gate, gate_index=bad).float().cpu()
+    nan_rows = torch.isnan(out).all(dim=1)
+    expect = torch.zeros(b * s, dtype=torch.bool)
+    for t in (3, 10):
+        expect[t::s] = True
+    assert torch.equal(nan_rows, expect)
+    assert torch.equal(out[~expect], ref.float().cpu()[~expect])
+
+
+def test_ffn_with_gate_index_equals_the_gathered_gate(dev):
+    m, h, f = 2 * 64, 256, 384
+    x, cu, su, bu, cd, sd, bd, _, res = ffn_inputs(m, h, 2 * f)
+    cd, sd = quantize_weight_rows(torch.randn((h, f), generator=torch.Generator().manual_seed(9)) * 0.02)
+    g = torch.Generator().manual_seed(43)
+    table = torch.rand((5, 6, h), generator=g).to(torch.bfloat16).to(dev)
+    index = torch.randint(0, 5, (64,), generator=g).to(dev)
+    ex = RowFP8Execution("w8a8", activation_quantizer="triton")
+    d = lambda t: t.to(dev)
+    args = (ex, d(x), d(cu), d(su), d(bu), d(cd), d(sd), d(bd))
+    got = fp8_ffn(*args, table[:, 5, :], d(res), activation="swiglu", gate_index=index)
+    ref = fp8_ffn(*args, table[:, 5, :].index_select(0, index).repeat(2, 1), d(res), activation="swiglu")
+    assert torch.equal(got, ref)

@@ -52,7 +52,8 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     ),
     "vflash_requant_rows_e4m3": ([_P, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P], _I32),
     "vflash_fp8_linear_gate_residual": (
-        [_P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _I64, _P],
+        [_P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _I64, _P, _I64,
+         _P, _I64, _P],
         _I32,
     ),
     "vflash_lora_down": ([_P, _I64, _I64, _I64, _P, _I64, _P, _P], _I32),
@@ -84,7 +85,7 @@ def library() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = restype
-    if lib.vflash_abi_version() != 1:
+    if lib.vflash_abi_version() != 2:
         raise RuntimeError("libvflash_amd.so has an unexpected ABI version")
     return lib
 

@@ -77,7 +77,7 @@ vfa::GemmParams base_params(const void* a, const float* sa, int64_t lda, const v
 
 extern "C" {
 
-int vflash_abi_version(void) { return 1; }
+int vflash_abi_version(void) { return 2; }
 
 const char* vflash_status_string(int s) {
   switch (s) {
@@ -211,18 +211,25 @@ int vflash_requant_rows_e4m3(const void* g, int64_t m, int64_t k, int64_t ldg,
 int vflash_fp8_linear_gate_residual(const void* a, const float* sa, int64_t lda, const void* w,
                                     const float* sw, int64_t ldw, int64_t m, int64_t n,
                                     int64_t k, const void* bias, const void* gate,
-                                    int64_t gate_ts, int64_t gate_hs, const void* residual,
-                                    int64_t ldr, void* out, int64_t ldo, void* stream) {
+                                    int64_t gate_ts, int64_t gate_hs, int64_t gate_tokens,
+                                    const int64_t* gate_index, int64_t gate_rows,
+                                    const void* residual, int64_t ldr, void* out, int64_t ldo,
+                                    void* stream) {
   if (!gemm_args_ok(a, sa, lda, w, sw, ldw, m, n, k, bias)) return VFLASH_EINVAL;
   if (!gate || !residual || !out || ldo < n || ldr < n || ldo % 4 || !aligned(out, 8))
     return VFLASH_EINVAL;
   if (gate_ts < 0 || gate_hs < 0 || !aligned(gate, 2) || !aligned(residual, 2))
+    return VFLASH_EINVAL;
+  if (gate_tokens < 1 || (gate_index && (gate_rows < 1 || !aligned(gate_index, 8))))
     return VFLASH_EINVAL;
   if (out == residual && ldo != ldr) return VFLASH_EINVAL;
   vfa::GemmParams p = base_params(a, sa, lda, w, sw, ldw, m, n, k, bias, out, ldo);
   p.gate = static_cast<const uint16_t*>(gate);
   p.gate_ts = gate_ts;
   p.gate_hs = gate_hs;
+  p.gate_tokens = gate_tokens;
+  p.gate_index = gate_index;
+  p.gate_rows = gate_rows;
   p.residual = static_cast<const uint16_t*>(residual);
   p.ldr = ldr;
   return status(vfa::launch_fp8_gemm(p, vfa::EPI_GATE, static_cast<hipStream_t>(stream)));

@@ -326,12 +326,25 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
       v4i v = *reinterpret_cast<const v4i*>(stage + row * PITCH + ((c ^ (row % CH)) << 4));
       if constexpr (EPI == EPI_GATE) {
         const uint16_t* res = p.residual + m * p.ldr + n;
-        const uint16_t* gt = p.gate + m * p.gate_ts + n * p.gate_hs;
+        // Gate row of output row m: token m % gate_tokens, through the index when
+        // one is given (the adaLN gather read in place).  An index outside
+        // [0, gate_rows) makes the row's gate NaN; nothing outside is read.
+        int64_t g = m % p.gate_tokens;
+        float bad = 0.0f;
+        if (p.gate_index) {
+          g = p.gate_index[g];
+          if ((uint64_t)g >= (uint64_t)p.gate_rows) {
+            g = 0;
+            bad = __builtin_nanf("");
+          }
+        }
+        const uint16_t* gt = p.gate + g * p.gate_ts + n * p.gate_hs;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const uint32_t y = (uint32_t)v[j];
-          const uint32_t gy = pack_bf16x2(bf16_to_f32(gt[(2 * j) * p.gate_hs]) * bf16_lo(y),
-                                          bf16_to_f32(gt[(2 * j + 1) * p.gate_hs]) * bf16_hi(y));
+          const uint32_t gy =
+              pack_bf16x2((bf16_to_f32(gt[(2 * j) * p.gate_hs]) + bad) * bf16_lo(y),
+                          (bf16_to_f32(gt[(2 * j + 1) * p.gate_hs]) + bad) * bf16_hi(y));
           v[j] = (int)pack_bf16x2(bf16_to_f32(res[2 * j]) + bf16_lo(gy),
                                   bf16_to_f32(res[2 * j + 1]) + bf16_hi(gy));
         }

@@ -21,8 +21,11 @@ struct GemmParams {
   int64_t plane_cols;    // > 0: column n goes to plane n / plane_cols
   int64_t plane_stride;  // elements between planes
   float* amax_part;      // EPI_GELU: [m, ceil(n / 64)] per-row maxima of |out|
-  const uint16_t* gate;  // EPI_GATE: gate[m * gate_ts + n * gate_hs]
-  int64_t gate_ts, gate_hs;
+  const uint16_t* gate;  // EPI_GATE: gate[g * gate_ts + n * gate_hs] for output row m, with
+  int64_t gate_ts, gate_hs;  // g = m % gate_tokens, or gate_index[m % gate_tokens] (< gate_rows)
+  int64_t gate_tokens;
+  const int64_t* gate_index;
+  int64_t gate_rows;
   const uint16_t* residual;  // EPI_GATE: residual[m * ldr + n]
   int64_t ldr;
   const uint16_t* lora_t;  // EPI_LORA: t[m * ldt + r], bf16

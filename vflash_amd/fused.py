@@ -143,11 +143,16 @@ def fp8_ffn(
     residual,
     *,
     activation: str = "gelu_tanh",
+    gate_index=None,
 ):
     """residual + gate * down(requant(act(up(value)))) with reference rounding.
 
     ``value`` and ``residual`` are ``[.., hidden]``; ``gate`` is ``[hidden]``
-    (broadcast over tokens) or ``[tokens, hidden]`` with any strides.
+    (broadcast over tokens), ``[T, hidden]`` with the rows a multiple of T (row
+    m uses gate row m % T), or, with ``gate_index`` (int64 ``[T]``, the
+    reference's ``adaln_indices``), the ungathered adaLN rows ``table[:, j, :]``
+    of which row m uses ``gate_index[m % T]`` (h3_native_denoiser.py:556-576
+    without the ``index_select`` copy).  Any strides.
     ``activation`` is ``"gelu_tanh"`` (up projection ``[F, hidden]``) or
     ``"swiglu"``, the H3 feed-forward (h3_native_denoiser.py:369-382, 563-576):
     the up projection is the packed ``[2F, hidden]`` value/gate matrix and the
@@ -179,7 +184,8 @@ def fp8_ffn(
         h_codes, h_scale = kernels.requant_rows(g, amax)
     with execution.measure("linear.fp8_gemm"):
         out = kernels.fp8_gemm_gate_residual(
-            h_codes, h_scale, down_weight, down_scale, rows, gate, res, down_bias
+            h_codes, h_scale, down_weight, down_scale, rows, gate, res, down_bias,
+            gate_index=gate_index,
         )
     return out.reshape(shape)
 
@@ -196,7 +202,7 @@ class FP8FeedForward(torch.nn.Module):
         self.up, self.down, self.execution = up, down, up.execution
         self.activation = activation
 
-    def forward(self, value, gate, residual):
+    def forward(self, value, gate, residual, gate_index=None):
         return fp8_ffn(
             self.execution,
             value,
@@ -209,6 +215,7 @@ class FP8FeedForward(torch.nn.Module):
             gate,
             residual,
             activation=self.activation,
+            gate_index=gate_index,
         )
 
 

@@ -198,29 +198,45 @@ def requant_rows(g, amax_part, pad_to: int = 16):
 
 
 def fp8_gemm_gate_residual(codes, act_scale, weight, w_scale, rows, gate, residual, bias=None,
-                           out=None):
-    """out = bf16(residual + bf16(gate * linear)); gate is [N] or [rows, N] (any strides)."""
+                           out=None, gate_index=None):
+    """out = bf16(residual + bf16(gate * linear)).
+
+    ``gate`` is ``[N]`` (one row for every token), ``[T, N]`` with ``rows`` a
+    multiple of T (row m uses gate row m % T: ``[rows, N]`` per row, ``[S, N]``
+    broadcast over a batch), or with ``gate_index`` (int64 ``[T]``) any ``[R, N]``
+    of which row m uses ``gate_index[m % T]`` (an adaLN table view gathered in
+    place).  Any strides.
+    """
     device = _gemm_operands(codes, act_scale, weight, w_scale, rows, bias)
     n, k = weight.shape
     if gate.dtype != torch.bfloat16 or residual.dtype != torch.bfloat16:
         raise ValueError("gate and residual must be BF16")
     if gate.ndim == 1:
-        if gate.shape != (n,):
+        if gate.shape != (n,) or gate_index is not None:
             raise ValueError("a broadcast gate must have the output width")
-        gts, ghs = 0, gate.stride(0)
-    elif gate.ndim == 2 and gate.shape == (rows, n):
-        gts, ghs = gate.stride(0), gate.stride(1)
+        gts, ghs, tokens, gate_rows = 0, gate.stride(0), 1, 1
+    elif gate.ndim == 2 and gate.shape[1] == n:
+        gts, ghs, gate_rows = gate.stride(0), gate.stride(1), gate.shape[0]
+        if gate_index is not None:
+            if gate_index.dtype != torch.int64 or gate_index.ndim != 1 or not gate_index.is_contiguous():
+                raise ValueError("gate indices must be a contiguous int64 vector")
+            tokens = gate_index.numel()
+        else:
+            tokens = gate.shape[0]
+        if tokens < 1 or rows % tokens:
+            raise ValueError("output rows must be a whole number of gated token blocks")
     else:
-        raise ValueError("gate must be [N] or [rows, N]")
+        raise ValueError("gate must be [N] or [T, N]")
     if residual.shape != (rows, n) or residual.stride(1) != 1:
         raise ValueError("residual must be [rows, N] with unit column stride")
-    require_device(gate, residual)
+    require_device(gate, residual, gate_index)
     if out is None:
         out = torch.empty((rows, n), device=device, dtype=torch.bfloat16)
     if rows:
         call("vflash_fp8_linear_gate_residual", ptr(codes), ptr(act_scale), codes.stride(0),
              ptr(weight), ptr(w_scale), weight.stride(0), rows, n, k, ptr(bias), ptr(gate), gts,
-             ghs, ptr(residual), residual.stride(0), ptr(out), out.stride(0), stream_of(device))
+             ghs, tokens, ptr(gate_index), gate_rows, ptr(residual), residual.stride(0), ptr(out),
+             out.stride(0), stream_of(device))
     return out
 
 
