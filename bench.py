@@ -11,8 +11,8 @@ HBM.  A step is one ``linear`` call; K timed steps are bracketed by
 events recorded on the launch stream around each of its launches in the timed
 region.  Prints one JSON line.
 
-Other workloads (``qkv``, ``ffn``, ``ffn_swiglu``, ``skinny``, ``nvfp4``, ``small``,
-``norm_quant``) print the same kind of line for the other shapes of this path; ``copy`` times a plain
+Other workloads (``qkv``, ``ffn``, ``ffn_swiglu``, ``skinny``, ``nvfp4`` (W4A4),
+``nvfp4_w4a8``, ``small``, ``norm_quant``) print the same kind of line for the other shapes of this path; ``copy`` times a plain
 1 GiB device copy, the calibration kernel for the HBM byte counters.  For the
 launch-bound shapes (``small``, ``skinny``) the line adds a device-side time
 per step measured with the launch queue filled ahead.
@@ -42,8 +42,8 @@ def parse():
     p.add_argument(
         "--workload",
         default="fp8_linear",
-        choices=["fp8_linear", "qkv", "ffn", "ffn_swiglu", "skinny", "nvfp4", "small", "norm_quant",
-                 "copy"],
+        choices=["fp8_linear", "qkv", "ffn", "ffn_swiglu", "skinny", "nvfp4", "nvfp4_w4a8", "small",
+                 "norm_quant", "copy"],
     )
     p.add_argument("--skinny-m", type=int, default=1024)
     p.add_argument("--skinny-n", type=int, default=6144)
@@ -333,31 +333,51 @@ def make_workload(args, dev):
              "operand_sets": count, "flops_per_step": 2.0 * m * n * k + 2.0 * m * r * (k + n)},
             launch_bound=True)
 
-    if wl == "nvfp4":
+    if wl in ("nvfp4", "nvfp4_w4a8"):
         from vflash_amd.nvfp4_linear import NVFP4Execution, NVFP4Weight
         from vflash_amd.prepare import quantize_nvfp4_weight
 
+        # W4A4 (the reference's arithmetic): NVFP4 activations with a calibrated
+        # global input scale (448 * 6 / amax), E2M1 weights with E4M3 block scales.
+        # nvfp4_w4a8: per-token E4M3 activations against the same weights.
+        w4a4 = wl == "nvfp4"
         m, k, n = 32760, 5120, 13824
         g = torch.Generator().manual_seed(0)
         x = torch.randn((m, k), generator=g).to(torch.bfloat16)
         w = torch.randn((n, k), generator=g) * 0.02
-        packed, scales, alpha, ins = quantize_nvfp4_weight(w)
+        input_scale = 2688.0 / float(x.float().abs().max())
+        packed, scales, alpha, ins = quantize_nvfp4_weight(w, input_scale)
         weight = NVFP4Weight(packed.to(dev), scales.to(dev), alpha.to(dev), ins.to(dev))
         xd = x.to(dev)
-        NVFP4Execution().linear(xd[:16], weight)
+        NVFP4Execution("nvfp4" if w4a4 else "e4m3").linear(xd[:16], weight)
+        out_scale = weight.alpha / weight.input_scale
 
         def step(i, timer):
-            a, sa = kernels.quantize_rows(xd)
+            if w4a4:
+                a, sa = kernels.nvfp4_quantize_rows(xd, weight.input_scale)
+            else:
+                a, sa = kernels.quantize_rows(xd)
             if timer:
                 timer.start()
-            kernels.nvfp4_gemm(a, sa, weight.packed, weight.scales, weight.alpha, m)
+            if w4a4:
+                kernels.nvfp4_w4a4_gemm(a, sa, weight.packed, weight.scales, out_scale, m)
+            else:
+                kernels.nvfp4_gemm(a, sa, weight.packed, weight.scales, weight.alpha, m)
             if timer:
                 timer.stop()
 
         flops = 2.0 * m * n * k
+        if w4a4:
+            return Workload(
+                wl, "NVFP4 W4A4 linear TFLOP/s (M=32760,K=5120,N=13824)", "TFLOP/s", flops, step,
+                "nvfp4_gemm_pipe<true>", flops, "mfma", BF16_PEAK_TFLOPS,
+                {"workload": "nvfp4_w4a4_linear_m32760_k5120_n13824", "m": m, "k": k, "n": n,
+                 "activations": "NVFP4 (e2m1 + e4m3 block-16 scales, global input scale)",
+                 "mfma": "f16 on exactly dequantized e2m1 x e4m3 operands"},
+                dtype="e2m1 x e2m1 with e4m3 block scales (f16 mfma, exact operands)")
         return Workload(
-            wl, "NVFP4-weight linear TFLOP/s (M=32760,K=5120,N=13824)", "TFLOP/s", flops, step,
-            "nvfp4_gemm", flops, "mfma", BF16_PEAK_TFLOPS,
+            wl, "NVFP4-weight W4A8 linear TFLOP/s (M=32760,K=5120,N=13824)", "TFLOP/s", flops, step,
+            "nvfp4_gemm_pipe<false>", flops, "mfma", BF16_PEAK_TFLOPS,
             {"workload": "nvfp4_weight_linear_m32760_k5120_n13824", "m": m, "k": k, "n": n,
              "mfma": "f16 on exactly dequantized e4m3 activations and e2m1 x e4m3 weights"},
             dtype="e4m3 activations x e2m1 weights (f16 mfma, exact operands)")

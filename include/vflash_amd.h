@@ -222,8 +222,9 @@ int vflash_fp8_linear_lora(const void* a, const float* sa, int64_t lda, const vo
 
 /*
  * NVFP4-weight linear (W4A8: E4M3 per-token activations, E2M1 weights with
- * E4M3 scales per 16-element K block and an fp32 output multiplier).
- * Replaces the mm_fp4 call of NVFP4Execution.linear
+ * E4M3 scales per 16-element K block and an fp32 output multiplier).  A more
+ * accurate alternative to the reference's W4A4 arithmetic
+ * (vflash_nvfp4_w4a4_linear), taking the place of the same mm_fp4 call
  *   (src/vflash/native/h3_nvfp4_linear.py:118-139).
  *   a        e4m3 [m, k] (lda);  sa fp32 [m]
  *   w_packed u8 [n, k/2]: element 2j in the low nibble, 2j+1 in the high nibble
@@ -236,6 +237,43 @@ int vflash_fp8_linear_lora(const void* a, const float* sa, int64_t lda, const vo
 int vflash_nvfp4_linear(const void* a, const float* sa, int64_t lda, const void* w_packed,
                         const void* w_scales, const float* alpha, int64_t m, int64_t n, int64_t k,
                         const void* bias, void* out, int64_t ldo, void* stream);
+
+/*
+ * NVFP4 activation quantization, the W4A4 input of the reference's NVFP4 linear.
+ * Replaces nvfp4_quantize(x, input_scale, sfLayout=128x4, do_shuffle=False)
+ *   (FlashInfer 0.6.18) as called at src/vflash/native/h3_nvfp4_linear.py:102-111.
+ *   x          bf16 [m, k] (f16 when x_is_f16), row stride ldx
+ *   global_sf  fp32 device scalar (NVFP4Weight.input_scale)
+ *   per 16-element K block, binary32:
+ *     sf    = e4m3(min(gsf * (amax * RN(1/6)), 448)),  scale = sf ? 1 / (sf * (1/gsf)) : 0
+ *     code  = e2m1(clamp(x * scale, -6, 6))  (round to nearest even, sign kept)
+ *   codes  u8 [m, k/2] (ldc bytes): element 2j in the low nibble
+ *   scales u8 (e4m3) [m_pad, k/16] in the 128x4 tiled order; m_pad is a multiple
+ *          of 128 >= m, and the padding rows' scales are 0 (the layout
+ *          h3_nvfp4_linear.py:103-111 checks).
+ *   Requires k % 64 == 0, ldx % 8 == 0, ldc % 16 == 0, ldc >= k/2, x and codes
+ *   16-byte aligned, scales and global_sf 4-byte aligned.
+ */
+int vflash_nvfp4_quantize_rows(const void* x, int x_is_f16, int64_t m, int64_t k, int64_t ldx,
+                               const float* global_sf, void* codes, int64_t ldc, void* scales,
+                               int64_t m_pad, void* stream);
+
+/*
+ * W4A4 NVFP4 linear: E2M1 activations and weights, each with E4M3 scales per
+ * 16-element K block in the 128x4 order, and one fp32 output scale.
+ * Replaces mm_fp4(codes, W^T, scales, W_scales^T, alpha, bf16, block_size=16,
+ *   backend="cutlass", use_nvfp4=True) followed by + bias
+ *   (src/vflash/native/h3_nvfp4_linear.py:114-139).
+ *   a        u8 [m, k/2] (lda bytes);  a_scales: as vflash_nvfp4_quantize_rows writes them
+ *   w_packed u8 [n, k/2];  w_scales u8 [n, k/16], 128x4 order (NVFP4Weight)
+ *   alpha    fp32 device scalar: NVFP4Weight.alpha / NVFP4Weight.input_scale
+ *   out = bf16(bf16(alpha * sum_k e2m1(a) e4m3(sa_blk) e2m1(w) e4m3(sw_blk)) + bias[n])
+ *   Requires n % 128 == 0, k % 64 == 0, lda % 16 == 0, a, w_packed, a_scales and
+ *   w_scales 16-byte aligned.
+ */
+int vflash_nvfp4_w4a4_linear(const void* a, int64_t lda, const void* a_scales, const void* w_packed,
+                             const void* w_scales, const float* alpha, int64_t m, int64_t n,
+                             int64_t k, const void* bias, void* out, int64_t ldo, void* stream);
 
 /*
  * Tuning hook: force a GEMM tile configuration for later calls in this process

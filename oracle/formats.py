@@ -99,13 +99,15 @@ E2M1_MAGNITUDES = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], dtype=np.fl
 
 
 def e2m1_encode(x) -> np.ndarray:
-    """Values within [-6, 6] -> E2M1 codes (RNE); sign bit set for negative inputs."""
+    """Values within [-6, 6] -> E2M1 codes (RNE); the sign bit follows the sign of
+    the input, -0 included (E2M1 has a negative zero, and a sign-preserving
+    conversion keeps it)."""
     x = np.asarray(x, dtype=np.float64)
     if np.any(np.abs(x) > 6.0):
         raise ValueError("E2M1 encode expects values clamped to [-6, 6]")
     r = round_to_grid(np.abs(x), 1, 0)
     code = np.searchsorted(E2M1_MAGNITUDES.astype(np.float64), r).astype(np.uint8)
-    return code | np.where(x < 0, 8, 0).astype(np.uint8)
+    return code | np.where(np.signbit(x), 8, 0).astype(np.uint8)
 
 
 def e2m1_decode(codes) -> np.ndarray:

@@ -1,13 +1,14 @@
-"""NVFP4-weight (W4A8) path restated on the CPU in numpy (test infrastructure).
+"""NVFP4 path restated on the CPU in numpy (test infrastructure).
 
 The reference's NVFP4 arithmetic lives in FlashInfer 0.6.18 (pyproject.toml:25;
 nvfp4_quantize / mm_fp4 with the CUTLASS backend, called at
 src/vflash/native/h3_nvfp4_linear.py:102-130), which is not vendored and not
 installed here.  PARITY UNPINNED against FlashInfer: the weight packing, the
-block-scale rounding and the 128x4 order below are this path's conventions
-(restating the published NVFP4 recipe and the 128x4 scale-tile formula), and
-they are pinned by closed forms, the OCP E2M1/E4M3 tables and brute force on
-small cases, not by reference vectors.
+activation quantization (FlashInfer's published per-block recipe, restated
+below with correctly rounded reciprocals where FlashInfer uses the hardware's
+approximate ones), the block-scale rounding and the 128x4 order are pinned by
+closed forms, the OCP E2M1/E4M3 tables and brute force on small cases, not by
+reference vectors.
 """
 
 from __future__ import annotations
@@ -66,13 +67,14 @@ def quantize_weight(w):
 
 
 def dequantize_weight(packed, tiled_scales) -> np.ndarray:
-    """Exact e2m1 * e4m3 block-scale values [N, K] (binary64), without alpha."""
+    """Exact e2m1 * e4m3 block-scale values [N, K] (binary64), without alpha.
+    ``tiled_scales`` may have more (padding) rows than ``packed``."""
     packed = np.asarray(packed, np.uint8)
     n, half = packed.shape
     q = np.empty((n, 2 * half), dtype=np.uint8)
     q[:, 0::2] = packed & 0xF
     q[:, 1::2] = packed >> 4
-    sf = e4m3_decode(unswizzle_128x4(tiled_scales)).astype(np.float64)
+    sf = e4m3_decode(unswizzle_128x4(tiled_scales)[:n]).astype(np.float64)
     return e2m1_decode(q).astype(np.float64) * np.repeat(sf, 16, axis=1)
 
 
@@ -81,6 +83,50 @@ def linear(a_codes, sa, packed, tiled_scales, alpha, bias=None):
     a = e4m3_decode(a_codes).astype(np.float64)
     acc = a @ dequantize_weight(packed, tiled_scales).T
     y = bf16_round(acc * np.asarray(sa, np.float64).reshape(-1, 1)[: acc.shape[0]] * float(alpha))
+    if bias is None:
+        return y
+    return bf16_round(y + np.asarray(bias, F32).reshape(1, -1))
+
+
+SIXTH = F32(1.0) / F32(6.0)  # RN(1/6)
+
+
+def quantize_activation(x, global_sf):
+    """NVFP4 activation quantization of nvfp4_quantize(x, input_scale) as the
+    reference calls it (h3_nvfp4_linear.py:102): per row and 16-element block,
+    in binary32,
+      sf    = e4m3(min(gsf * (amax_block * RN(1/6)), 448))     (RNE, satfinite)
+      scale = sf != 0 ? 1 / (sf * (1 / gsf)) : 0
+      q     = e2m1(clamp(x * scale, -6, 6))                    (RNE, satfinite)
+    FlashInfer forms the two reciprocals with the hardware's approximate
+    reciprocal; here they are correctly rounded (parity unpinned: a one-ulp
+    difference of ``scale`` moves a code only next to an E2M1 rounding
+    boundary).  Returns packed codes [M, K/2] (element 2j in the low nibble)
+    and block scales in the 128x4 order with the rows padded to a multiple of
+    128 (padding scales 0), the layout h3_nvfp4_linear.py:103-111 checks."""
+    x = np.asarray(x, F32)
+    m, k = x.shape
+    gsf = F32(global_sf)
+    blocks = x.reshape(m, k // 16, 16)
+    bmax = np.max(np.abs(blocks), axis=-1)
+    sf = e4m3_encode(np.minimum(gsf * (bmax * SIXTH), F32(448.0)))
+    sf_f = e4m3_decode(sf)
+    with np.errstate(divide="ignore", over="ignore"):
+        scale = np.where(sf_f > 0, F32(1.0) / (sf_f * (F32(1.0) / gsf)), F32(0.0)).astype(F32)
+    q = e2m1_encode(np.clip(blocks * scale[..., None], F32(-6.0), F32(6.0))).reshape(m, k)
+    packed = (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
+    m_pad = -(-m // 128) * 128
+    plain = np.zeros((m_pad, k // 16), dtype=np.uint8)
+    plain[:m] = sf
+    return packed, swizzle_128x4(plain)
+
+
+def linear_w4a4(a_packed, a_tiled_scales, packed, tiled_scales, alpha, bias=None):
+    """mm_fp4 then + bias (h3_nvfp4_linear.py:114-139): bf16(alpha * sum_k a_dq *
+    w_dq) with an exact sum, then bf16(y + bias).  ``alpha`` is the output
+    scale, weight.alpha / weight.input_scale."""
+    acc = dequantize_weight(a_packed, a_tiled_scales) @ dequantize_weight(packed, tiled_scales).T
+    y = bf16_round(acc * float(alpha))
     if bias is None:
         return y
     return bf16_round(y + np.asarray(bias, F32).reshape(1, -1))

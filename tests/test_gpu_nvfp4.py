@@ -1,4 +1,5 @@
-"""NVFP4-weight (W4A8) linear on gfx950 against the oracle."""
+"""NVFP4 linear on gfx950 against the oracle: the W4A8 variant (E4M3 activations)
+and the reference's W4A4 arithmetic (NVFP4 activations, the default)."""
 
 import numpy as np
 import pytest
@@ -7,7 +8,7 @@ import torch
 from oracle import fp8 as O
 from oracle import nvfp4 as N
 from tests.conftest import rel_check
-from vflash_amd import _lib
+from vflash_amd import _lib, kernels
 from vflash_amd.nvfp4_linear import NVFP4Execution, NVFP4Weight
 from vflash_amd.prepare import quantize_nvfp4_weight
 
@@ -37,11 +38,11 @@ def tile():
 
 @pytest.mark.parametrize("cfg", [1, 2, 3, 4])
 @pytest.mark.parametrize("m,n,k", [(1, 128, 64), (37, 256, 192), (300, 384, 512), (513, 640, 1088)])
-def test_small_shapes_every_tile(dev, tile, cfg, m, n, k):
+def test_w4a8_small_shapes_every_tile(dev, tile, cfg, m, n, k):
     _lib.set_gemm_tile(cfg)
     x, (packed, scales, alpha, ins), b = make(m, n, k, seed=m + n + k)
     weight = NVFP4Weight(packed.to(dev), scales.to(dev), alpha.to(dev), ins.to(dev))
-    ex = NVFP4Execution()
+    ex = NVFP4Execution("e4m3")
     out = ex.linear(x.to(dev), weight, b.to(dev))
     rel_check(out.float().cpu().numpy(), oracle(x, packed, scales, alpha, b))
     out = ex.linear(x.to(dev), weight)
@@ -49,19 +50,121 @@ def test_small_shapes_every_tile(dev, tile, cfg, m, n, k):
     assert ex.calls == 2 and ex.rows == 2 * m
 
 
-def test_fp32_and_3d_inputs(dev):
+def test_w4a8_fp32_and_3d_inputs(dev):
     x, (packed, scales, alpha, ins), b = make(2 * 3 * 32, 128, 256)
     weight = NVFP4Weight(packed.to(dev), scales.to(dev), alpha.to(dev), ins.to(dev))
-    out = NVFP4Execution().linear(x.float().reshape(2, 96, 256).to(dev), weight, b.to(dev))
+    out = NVFP4Execution("e4m3").linear(x.float().reshape(2, 96, 256).to(dev), weight, b.to(dev))
     assert out.shape == (2, 96, 128) and out.dtype == torch.bfloat16
     rel_check(out.reshape(-1, 128).float().cpu().numpy(), oracle(x, packed, scales, alpha, b))
 
 
-def test_config_shape_sampled_rows(dev):
+def test_w4a8_config_shape_sampled_rows(dev):
     # X [32760, 5120] per-token e4m3; W e2m1 [13824, 5120] + e4m3 block-16 scales + fp32 global.
     x, (packed, scales, alpha, ins), _ = make(32760, 13824, 5120, bias=False)
     weight = NVFP4Weight(packed.to(dev), scales.to(dev), alpha.to(dev), ins.to(dev))
-    out = NVFP4Execution().linear(x.to(dev), weight)
+    out = NVFP4Execution("e4m3").linear(x.to(dev), weight)
     rows = np.r_[0:8, 12000:12008, 32752:32760]
     rel_check(out.float().cpu().numpy()[rows], oracle(x, packed, scales, alpha, None, rows))
     assert bool(torch.isfinite(out.float()).all())
+
+
+
+# --- W4A4: NVFP4 activations (the reference's arithmetic) ---------------------
+
+def w4a4_oracle(x, packed, scales, alpha, input_scale, b, rows=None):
+    xs = x.float().numpy() if rows is None else x.float().numpy()[rows]
+    a, sa = N.quantize_activation(xs, input_scale)
+    out_scale = np.float32(alpha) / np.float32(input_scale)  # one fp32 division, as on the device
+    return N.linear_w4a4(a, sa, packed.numpy(), scales.numpy(), out_scale,
+                         None if b is None else b.float().numpy())
+
+
+@pytest.mark.parametrize("m,k", [(1, 64), (37, 192), (300, 512), (129, 1088)])
+@pytest.mark.parametrize("gsf", [1.0, 0.37, None])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_activation_quantizer_is_bit_exact(dev, m, k, gsf, dtype):
+    g = torch.Generator().manual_seed(m * k)
+    x = (torch.randn((m, k), generator=g) * 3).to(dtype)
+    x[0, :16] = 0.0  # a zero block: scale 0, codes 0
+    if m > 1:
+        x[1, 16:32] = -0.0
+        x[1, 5] = 1e-30  # far below the block's grid
+    if gsf is None:
+        gsf = 2688.0 / float(x.float().abs().max())  # the calibrated global scale 448 * 6 / amax
+    sf = torch.tensor(gsf, dtype=torch.float32)
+    codes, scales = kernels.nvfp4_quantize_rows(x.to(dev), sf.to(dev))
+    rc, rs = N.quantize_activation(x.float().numpy(), np.float32(gsf))
+    assert codes.shape == (m, k // 2) and scales.shape == ((m + 127) // 128 * 128, k // 16)
+    assert np.array_equal(codes.cpu().numpy(), rc)
+    assert np.array_equal(scales.cpu().numpy(), rs)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 128, 64), (37, 256, 192), (300, 384, 512), (513, 640, 1088)])
+def test_w4a4_gemm_on_the_kernel_codes(dev, m, n, k):
+    x, (packed, scales, alpha, _), b = make(m, n, k, seed=3 * m + n)
+    gsf = torch.tensor(2688.0 / float(x.float().abs().max()), dtype=torch.float32)
+    codes, a_scales = kernels.nvfp4_quantize_rows(x.to(dev), gsf.to(dev))
+    out_scale = (alpha / gsf).to(dev)
+    out = kernels.nvfp4_w4a4_gemm(codes, a_scales, packed.to(dev), scales.to(dev), out_scale, m, b.to(dev))
+    ref = N.linear_w4a4(codes.cpu().numpy(), a_scales.cpu().numpy(), packed.numpy(), scales.numpy(),
+                        float(out_scale.cpu()), b.float().numpy())
+    rel_check(out.float().cpu().numpy(), ref)
+
+
+def test_w4a4_execution_is_the_default_and_matches_the_oracle_chain(dev):
+    m, n, k = 2 * 3 * 32, 256, 320
+    x, (packed, scales, alpha, _), b = make(m, n, k, seed=5)
+    input_scale = torch.tensor(2688.0 / float(x.float().abs().max()), dtype=torch.float32)
+    weight = NVFP4Weight(packed.to(dev), scales.to(dev), alpha.to(dev), input_scale.to(dev))
+    ex = NVFP4Execution()
+    assert ex.activations == "nvfp4" and "w4a4" in ex.contract
+    out = ex.linear(x.reshape(2, 96, k).to(dev), weight, b.to(dev))
+    assert out.shape == (2, 96, n) and ex.calls == 1 and ex.rows == m
+    rel_check(out.reshape(m, n).float().cpu().numpy(),
+              w4a4_oracle(x, packed, scales, float(alpha), float(input_scale), b))
+    # fp32 inputs are cast to bf16 first; f16 inputs are quantized as they are.
+    out32 = ex.linear(x.float().to(dev), weight, b.to(dev))
+    assert torch.equal(out32, out.reshape(m, n))
+    out16 = ex.linear(x.half().to(dev), weight)
+    ref16 = N.linear_w4a4(*N.quantize_activation(x.half().float().numpy(), np.float32(input_scale)),
+                          packed.numpy(), scales.numpy(), np.float32(alpha) / np.float32(input_scale))
+    rel_check(out16.float().cpu().numpy(), ref16)
+
+
+def test_calibrated_input_scale_and_weight_alpha_reach_the_kernel(dev):
+    # The reference's contract test: alpha 2.0, input_scale 4.0 -> output scale 0.5
+    # (tests/test_h3_nvfp4_linear.py:17-45), here through the real kernels.
+    m, n, k = 6, 128, 64
+    x, (packed, scales, _, _), b = make(m, n, k, seed=9)
+    weight = NVFP4Weight(packed.to(dev), scales.to(dev), torch.tensor(2.0).to(dev), torch.tensor(4.0).to(dev))
+    out = NVFP4Execution().linear(x.to(dev), weight, b.to(dev))
+    rel_check(out.float().cpu().numpy(), w4a4_oracle(x, packed, scales, 2.0, 4.0, b))
+    a, sa = N.quantize_activation(x.float().numpy(), np.float32(4.0))
+    assert sa.shape == (128, 4)  # padded to 128 rows, as the reference checks
+
+
+def test_w4a4_config_shape_sampled_rows(dev):
+    # X [32760, 5120] -> NVFP4 with a calibrated input scale; W e2m1 [13824, 5120].
+    x, (packed, scales, alpha, _), _ = make(32760, 13824, 5120, bias=False)
+    input_scale = torch.tensor(2688.0 / float(x.float().abs().max()), dtype=torch.float32)
+    weight = NVFP4Weight(packed.to(dev), scales.to(dev), alpha.to(dev), input_scale.to(dev))
+    out = NVFP4Execution().linear(x.to(dev), weight)
+    rows = np.r_[0:8, 12000:12008, 32752:32760]
+    rel_check(out.float().cpu().numpy()[rows],
+              w4a4_oracle(x, packed, scales, float(alpha), float(input_scale), None, rows))
+    assert bool(torch.isfinite(out.float()).all())
+
+
+def test_hardware_e2m1_conversion_is_rne_on_every_clamped_binary32(dev):
+    import subprocess
+    from pathlib import Path
+
+    probe = Path(__file__).resolve().parent / "probes" / "bin" / "e2m1_convert"
+    if not probe.exists():
+        pytest.fail("probe not built: run __graft_entry__.build()")
+    result = subprocess.run([str(probe)], capture_output=True, text=True, timeout=120)
+    assert result.returncode == 0, result.stdout + result.stderr
+    f = result.stdout.split()
+    assert f[0] == "values" and int(f[1]) == 2 * (0x40C00000 + 1), result.stdout
+    assert f[2] == "mismatches" and int(f[3]) == 0, result.stdout
+    assert f[4] == "order_mismatches" and int(f[5]) == 0, result.stdout

@@ -66,3 +66,47 @@ def test_nvfp4_linear_oracle_matches_brute_force():
             from oracle.formats import bf16_round
 
             assert got[i, j] == bf16_round(acc * float(sa[i]) * float(alpha))
+
+
+def test_activation_quantizer_is_exact_on_scaled_grid_blocks():
+    # Blocks of E2M1 grid values with |max| = 6 times 2^e (gsf = 1): the block
+    # scale is exactly 2^e (6 * RN(1/6) rounds to 1), the codes are the grid
+    # values, and the round trip is exact.  A dropped /6, a transposed scale or
+    # a swapped nibble order fails here.
+    rng = np.random.default_rng(5)
+    grid = np.array([0, 0.5, 1, 1.5, 2, 3, 4, 6], np.float32)
+    rows = []
+    for e in range(-9, 9):
+        v = grid[rng.integers(0, 8, (3, 16))] * np.where(rng.random((3, 16)) < 0.5, -1, 1)
+        v[:, rng.integers(0, 16)] = 6.0
+        rows.append((v * np.float32(2.0**e)).reshape(1, 48))
+    x = np.concatenate(rows).astype(np.float32)
+    x = np.concatenate([x, np.zeros((18, 16), np.float32)], axis=1)  # one zero block per row
+    packed, tiled = N.quantize_activation(x, np.float32(1.0))
+    assert tiled.shape == (128, 4)
+    plain = N.unswizzle_128x4(tiled)
+    assert np.all(plain[18:] == 0)
+    expect_sf = np.array([[0x38 + 8 * e if e >= -6 else 1 << (e + 9) for _ in range(3)] + [0]
+                          for e in range(-9, 9)])
+    assert np.array_equal(plain[:18], expect_sf)
+    assert np.array_equal(N.dequantize_weight(packed, tiled), x.astype(np.float64))
+
+
+def test_activation_quantizer_invariants_on_calibrated_rows():
+    rng = np.random.default_rng(6)
+    x = (rng.standard_normal((40, 256)) * rng.uniform(0.1, 10, (40, 1))).astype(np.float32)
+    gsf = np.float32(2688.0) / np.float32(np.abs(x).max())
+    packed, tiled = N.quantize_activation(x, gsf)
+    sf = e4m3_decode(N.unswizzle_128x4(tiled)[:40]).astype(np.float64)
+    q = np.empty((40, 256), np.uint8)
+    q[:, 0::2], q[:, 1::2] = packed & 0xF, packed >> 4
+    normal = sf >= 2.0**-6
+    # The block maximum always encodes as +-6 when the block scale is normal.
+    top = (q.reshape(40, 16, 16) & 7).max(axis=-1)
+    assert np.all(top[normal] == 7)
+    # Round-trip error: at most half the widest E2M1 step (2) of the block's
+    # scale, i.e. amax_block / 6 times the scale rounding (1 + 2^-4).
+    dq = N.dequantize_weight(packed, tiled) / float(gsf)
+    bmax = np.abs(x).reshape(40, 16, 16).max(axis=-1)
+    err = np.abs(dq - x).reshape(40, 16, 16).max(axis=-1)
+    assert np.all(err[normal] <= bmax[normal] / 6 * (1 + 2.0**-4) * (1 + 1e-6))

@@ -67,6 +67,11 @@ SIGNATURES: dict[str, tuple[list, object]] = {
         [_P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _P],
         _I32,
     ),
+    "vflash_nvfp4_quantize_rows": ([_P, _I32, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P], _I32),
+    "vflash_nvfp4_w4a4_linear": (
+        [_P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _P],
+        _I32,
+    ),
 }
 
 

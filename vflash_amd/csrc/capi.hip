@@ -21,6 +21,11 @@ hipError_t launch_lora_down(const uint16_t*, int64_t, int64_t, int64_t, const ui
                             uint16_t*, hipStream_t);
 hipError_t launch_quant_lora(const uint16_t*, int64_t, int64_t, int64_t, const uint16_t*, int,
                              uint16_t*, uint8_t*, float*, int64_t, hipStream_t);
+hipError_t launch_nvfp4_quant(const uint16_t*, bool, int64_t, int64_t, int64_t, const float*,
+                              uint8_t*, int64_t, uint8_t*, int64_t, hipStream_t);
+hipError_t launch_nvfp4_w4a4(const uint8_t*, int64_t, const uint8_t*, const uint8_t*,
+                             const uint8_t*, const float*, int64_t, int64_t, int64_t,
+                             const uint16_t*, uint16_t*, int64_t, int, hipStream_t);
 hipError_t launch_nvfp4(const uint8_t*, const float*, int64_t, const uint8_t*, const uint8_t*,
                         const float*, int64_t, int64_t, int64_t, const uint16_t*, uint16_t*, int64_t, int,
                         int, hipStream_t);
@@ -303,6 +308,38 @@ int vflash_nvfp4_linear(const void* a, const float* sa, int64_t lda, const void*
                                   static_cast<const uint16_t*>(bias),
                                   static_cast<uint16_t*>(out), ldo, tile, g_group_m,
                                   static_cast<hipStream_t>(stream)));
+}
+
+int vflash_nvfp4_quantize_rows(const void* x, int x_is_f16, int64_t m, int64_t k, int64_t ldx,
+                               const float* global_sf, void* codes, int64_t ldc, void* scales,
+                               int64_t m_pad, void* stream) {
+  if (!x || !global_sf || !codes || !scales || m < 1 || k < 64 || k % 64) return VFLASH_EINVAL;
+  if (ldx < k || ldx % 8 || ldc < k / 2 || ldc % 16 || m_pad < m || m_pad % 128) return VFLASH_EINVAL;
+  if (m_pad >= (int64_t(1) << 33)) return VFLASH_EINVAL;
+  if (!aligned(x, 16) || !aligned(codes, 16) || !aligned(scales, 4) || !aligned(global_sf, 4))
+    return VFLASH_EINVAL;
+  return status(vfa::launch_nvfp4_quant(static_cast<const uint16_t*>(x), x_is_f16 != 0, m, k, ldx,
+                                        global_sf, static_cast<uint8_t*>(codes), ldc,
+                                        static_cast<uint8_t*>(scales), m_pad,
+                                        static_cast<hipStream_t>(stream)));
+}
+
+int vflash_nvfp4_w4a4_linear(const void* a, int64_t lda, const void* a_scales, const void* w_packed,
+                             const void* w_scales, const float* alpha, int64_t m, int64_t n,
+                             int64_t k, const void* bias, void* out, int64_t ldo, void* stream) {
+  if (!a || !a_scales || !w_packed || !w_scales || !alpha || !out || m < 1 || n < 128 || k < 64)
+    return VFLASH_EINVAL;
+  if (n % 128 || k % 64 || lda < k / 2 || lda % 16 || ldo < n || ldo % 4) return VFLASH_EINVAL;
+  if (!aligned(a, 16) || !aligned(a_scales, 16) || !aligned(w_packed, 16) ||
+      !aligned(w_scales, 16) || !aligned(out, 8) || !aligned(alpha, 4))
+    return VFLASH_EINVAL;
+  if (bias && !aligned(bias, 2)) return VFLASH_EINVAL;
+  if (256 * lda >= (int64_t(1) << 31)) return VFLASH_EINVAL;
+  return status(vfa::launch_nvfp4_w4a4(
+      static_cast<const uint8_t*>(a), lda, static_cast<const uint8_t*>(a_scales),
+      static_cast<const uint8_t*>(w_packed), static_cast<const uint8_t*>(w_scales), alpha, m, n, k,
+      static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(out), ldo, g_group_m,
+      static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

@@ -185,4 +185,15 @@ __device__ __forceinline__ float e2m1_to_f32(uint32_t c) {
   return __uint_as_float(bits | ((c & 8u) << 28));
 }
 
+// binary32 -> OCP E2M1 code, round to nearest even on the clamped range
+// |f| <= 6 (values 0, 0.5, 1, 1.5, 2, 3, 4, 6; ties 0.25 -> 0, 0.75 -> 1,
+// 1.25 -> 1, 1.75 -> 2, 2.5 -> 2, 3.5 -> 4, 5 -> 4), sign in bit 3 (-0 keeps
+// it).  The reference encoder of the on-device conversion check.
+__device__ __forceinline__ uint32_t f32_to_e2m1(float f) {
+  const float a = fabsf(f);
+  const uint32_t c = (a > 0.25f) + (a >= 0.75f) + (a > 1.25f) + (a >= 1.75f) + (a > 2.5f) +
+                     (a >= 3.5f) + (a > 5.0f);
+  return c | ((__float_as_uint(f) >> 28) & 8u);
+}
+
 }  // namespace vfa

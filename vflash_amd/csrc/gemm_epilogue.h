@@ -119,7 +119,7 @@ __device__ __forceinline__ void stage_vectors(const GemmParams& p, int64_t m0, i
   if (wave == 0) {
     const uint32_t bytes = p.sw_step ? (uint32_t)(min((int64_t)BN, p.n - n0) * 4) : 4u;
     lds_dma16(make_rsrc(p.sw + (p.sw_step ? n0 : 0), bytes), vec_lds, (uint32_t)lane * 16);
-  } else if (wave == 1) {
+  } else if (wave == 1 && p.sa) {
     lds_dma16(make_rsrc(p.sa + m0, (uint32_t)(min((int64_t)BM, p.m - m0) * 4)), vec_lds + 1024,
               (uint32_t)lane * 16);
   } else if (wave == 2 && p.bias) {
@@ -153,7 +153,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
   float sam[MB];
   static_for<MB>([&](auto mb) {
     const int row = wm * WM + mb * 32 + fr;
-    if constexpr (VEC) {
+    // No row scales (sa null): a row factor of one, which changes nothing.
+    if (!sa_p) {
+      sam[mb] = 1.0f;
+    } else if constexpr (VEC) {
       sam[mb] = reinterpret_cast<const float*>(vec + 1024)[row];
     } else {
       sam[mb] = m0 + row < p.m ? sa_p[m0 + row] : 0.0f;

@@ -14,6 +14,8 @@ struct GemmParams {
   const float* sw;   // weight scales: sw[n * sw_step] (sw_step 0: one scalar)
   int64_t sw_step;
   const uint8_t* wsb;  // E2M1-weight GEMM: E4M3 block scales in the 128x4 order
+  const uint8_t* asb;  // E2M1 activations (W4A4): their block scales, 128x4 order, rows
+                       // padded to a multiple of 128; then sa is null
   int64_t lda, ldw, m, n, k;
   const uint16_t* bias;  // bf16 [n] or null
   uint16_t* out;         // bf16, row stride ldo elements

@@ -226,17 +226,29 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_kernel(const Fp4Params p) {
 // MFMA step v of a 64-K half u, lanes 0-31 supply K 64u + 8v .. +7 and lanes
 // 32-63 supply K 64u + 32 + 8v .. +7, so each lane reads 32 contiguous codes
 // and 16 contiguous packed bytes (one or two 16-element scale blocks) per half.
+//
+// W4A4 (A4 = true, the reference's mm_fp4 arithmetic): A is packed E2M1 with
+// its own 128x4 block scales, staged and dequantized exactly as W; the slot is
+// A 16 KB + W 16 KB + W scales 2 KB + A scales 2 KB, and the epilogue applies
+// the one output scale alpha (no per-row scale).
 constexpr int FP4_A = 256 * 128;
 constexpr int FP4_W = 256 * 64;
 constexpr int FP4_S = 2 * 1024;
-constexpr int FP4_SLOT = FP4_A + FP4_W + FP4_S;
 constexpr int FP4_LDS = 256 * 256 * 2;  // also the epilogue's bf16 staging tile
-static_assert(2 * FP4_SLOT <= FP4_LDS, "ring fits the staging buffer");
+template <bool A4>
+constexpr int fp4_a_bytes() { return A4 ? FP4_W : FP4_A; }
+template <bool A4>
+constexpr int fp4_slot() { return fp4_a_bytes<A4>() + FP4_W + FP4_S + (A4 ? FP4_S : 0); }
+static_assert(2 * fp4_slot<false>() <= FP4_LDS && 2 * fp4_slot<true>() <= FP4_LDS,
+              "ring fits the staging buffer");
 
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
+template <bool A4>
 __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
+  constexpr int SA = fp4_a_bytes<A4>(), FP4_SLOT = fp4_slot<A4>();
+  constexpr int OFF_W = SA, OFF_WS = SA + FP4_W, OFF_AS = SA + FP4_W + FP4_S;
   __shared__ __attribute__((aligned(1024))) uint8_t ring[FP4_LDS];
   __shared__ __attribute__((aligned(1024))) uint8_t vec[VEC_LDS];
   constexpr int MB = 4, NB = 4;
@@ -255,6 +267,11 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w + n0 * p.ldw, (uint32_t)(rows_w * p.ldw));
   const __amdgpu_buffer_rsrc_t rs =
       make_rsrc(p.wsb + (n0 / 128) * k_tiles * 512, (uint32_t)((rows_w / 128) * k_tiles * 512));
+  // A4: the A scales' 128-row tiles of this block (the caller pads the rows to 128).
+  const __amdgpu_buffer_rsrc_t ras =
+      A4 ? make_rsrc(p.asb + (m0 / 128) * k_tiles * 512,
+                     (uint32_t)(((rows_a + 127) / 128) * k_tiles * 512))
+         : rs;
 
   // DMA lane maps.  A: 1 KB block i of a wave = rows wave*64 + 8i .. +7, lane l
   // fills row + l/8, slot l%8 with logical chunk (l%8) ^ lds_swizzle(row).
@@ -268,36 +285,50 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
   const int wch = (lane & 3) ^ ((lane >> 4) & 3);
   const uint32_t w_base = (uint32_t)((wave * 64 + (lane >> 2)) * p.ldw + wch * 16);
   const uint32_t w_step = (uint32_t)(16 * p.ldw);
-  // Scales: waves 0 and 1 copy the stage's 1 KB (K tiles 2s, 2s+1) of row tile `wave`.
-  const uint32_t s_base = (uint32_t)(wave * k_tiles * 512 + lane * 16);
-  const uint32_t dst_a = ring_lds + wave * 8192, dst_w = ring_lds + FP4_A + wave * 4096;
-  const uint32_t dst_s = ring_lds + FP4_A + FP4_W + wave * 1024;
+  // Scales: waves 0 and 1 copy the stage's 1 KB (K tiles 2s, 2s+1) of W row tile
+  // wave & 1; with A4, waves 2 and 3 do the same for A.
+  const uint32_t dst_a = ring_lds + wave * (A4 ? 4096 : 8192), dst_w = ring_lds + OFF_W + wave * 4096;
+  const uint32_t dst_s = ring_lds + OFF_WS + (wave & 1) * 1024;
+  const uint32_t dst_as = ring_lds + OFF_AS + (wave & 1) * 1024;
+  const uint32_t s_base_any = (uint32_t)((wave & 1) * k_tiles * 512 + lane * 16);
   const int KT = (int)((p.k + 127) / 128);
 
   auto issue = [&](int j, int s) {
     const uint32_t slot = (uint32_t)j * FP4_SLOT;
     const int64_t kb = (int64_t)s * 128;
-    const uint32_t kill0 = kb + ach0 * 16 < p.k ? 0u : VFA_OOB;
-    const uint32_t kill1 = kb + ach1 * 16 < p.k ? 0u : VFA_OOB;
-    static_for<8>([&](auto i) {
-      const uint32_t off = (i % 2 ? a_base1 : a_base0) + (i / 2) * a_step + (uint32_t)kb;
-      lds_dma16(ra, dst_a + slot + i * 1024, off | (i % 2 ? kill1 : kill0));
-    });
     const int64_t kw = kb / 2;
-    const uint32_t killw = kw + wch * 16 < p.ldw ? 0u : VFA_OOB;
+    const uint32_t killw = kw + wch * 16 < p.k / 2 ? 0u : VFA_OOB;
+    if constexpr (A4) {
+      // 64-byte packed rows, the W map with A's row stride.
+      const uint32_t a4_base = (uint32_t)((wave * 64 + (lane >> 2)) * p.lda + wch * 16);
+      static_for<4>([&](auto i) {
+        lds_dma16(ra, dst_a + slot + i * 1024,
+                  (a4_base + i * (uint32_t)(16 * p.lda) + (uint32_t)kw) | killw);
+      });
+    } else {
+      const uint32_t kill0 = kb + ach0 * 16 < p.k ? 0u : VFA_OOB;
+      const uint32_t kill1 = kb + ach1 * 16 < p.k ? 0u : VFA_OOB;
+      static_for<8>([&](auto i) {
+        const uint32_t off = (i % 2 ? a_base1 : a_base0) + (i / 2) * a_step + (uint32_t)kb;
+        lds_dma16(ra, dst_a + slot + i * 1024, off | (i % 2 ? kill1 : kill0));
+      });
+    }
     static_for<4>([&](auto i) {
       lds_dma16(rw, dst_w + slot + i * 1024, (w_base + i * w_step + (uint32_t)kw) | killw);
     });
+    const uint32_t kills = 2 * (int64_t)s + (lane >> 5) < k_tiles ? 0u : VFA_OOB;
     if (wave < 2) {
-      const uint32_t kills = 2 * (int64_t)s + (lane >> 5) < k_tiles ? 0u : VFA_OOB;
-      lds_dma16(rs, dst_s + slot, (s_base + (uint32_t)s * 1024) | kills);
+      lds_dma16(rs, dst_s + slot, (s_base_any + (uint32_t)s * 1024) | kills);
+    } else if constexpr (A4) {
+      lds_dma16(ras, dst_as + slot, (s_base_any + (uint32_t)s * 1024) | kills);
     }
   };
 
   const int fr = lane & 31, fh = lane >> 5;
   const int asw = lds_swizzle(fr), wsw = (fr >> 2) & 3;
   struct Raw {
-    v4i a[MB][2];
+    v4i a[MB][A4 ? 1 : 2];
+    uint32_t as[A4 ? MB : 1];
     v4i w[NB];
     uint32_t s[NB];
   };
@@ -305,14 +336,21 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
   auto read_raw = [&](Raw& r, int j, auto u) {
     const uint8_t* base = ring + j * FP4_SLOT;
     static_for<MB>([&](auto mb) {
-      const uint8_t* row = base + (wm * 128 + mb * 32 + fr) * 128;
-      r.a[mb][0] = *reinterpret_cast<const v4i*>(row + (((4 * u + 2 * fh) ^ asw) << 4));
-      r.a[mb][1] = *reinterpret_cast<const v4i*>(row + (((4 * u + 2 * fh + 1) ^ asw) << 4));
+      if constexpr (A4) {
+        const uint8_t* row = base + (wm * 128 + mb * 32 + fr) * 64;
+        r.a[mb][0] = *reinterpret_cast<const v4i*>(row + (((2 * u + fh) ^ wsw) << 4));
+        r.as[mb] = *reinterpret_cast<const uint32_t*>(base + OFF_AS + wm * 1024 + u * 512 +
+                                                      fr * 16 + mb * 4);
+      } else {
+        const uint8_t* row = base + (wm * 128 + mb * 32 + fr) * 128;
+        r.a[mb][0] = *reinterpret_cast<const v4i*>(row + (((4 * u + 2 * fh) ^ asw) << 4));
+        r.a[mb][1] = *reinterpret_cast<const v4i*>(row + (((4 * u + 2 * fh + 1) ^ asw) << 4));
+      }
     });
     static_for<NB>([&](auto nb) {
-      const uint8_t* row = base + FP4_A + (wn * 128 + nb * 32 + fr) * 64;
+      const uint8_t* row = base + OFF_W + (wn * 128 + nb * 32 + fr) * 64;
       r.w[nb] = *reinterpret_cast<const v4i*>(row + (((2 * u + fh) ^ wsw) << 4));
-      r.s[nb] = *reinterpret_cast<const uint32_t*>(base + FP4_A + FP4_W + wn * 1024 + u * 512 +
+      r.s[nb] = *reinterpret_cast<const uint32_t*>(base + OFF_WS + wn * 1024 + u * 512 +
                                                    fr * 16 + nb * 4);
     });
   };
@@ -322,26 +360,31 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
   // MFMA step v (0..3) of a half held in r.
   auto step = [&](const Raw& r, auto v) {
     v8h xa[MB], xw[NB];
-    static_for<MB>([&](auto mb) {
-      const uint32_t d0 = (uint32_t)r.a[mb][v / 2][(v % 2) * 2];
-      const uint32_t d1 = (uint32_t)r.a[mb][v / 2][(v % 2) * 2 + 1];
-      const v2h x0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, false);
-      const v2h x1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, true);
-      const v2h x2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, false);
-      const v2h x3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, true);
-      xa[mb] = v8h{x0[0], x0[1], x1[0], x1[1], x2[0], x2[1], x3[0], x3[1]};
-    });
-    static_for<NB>([&](auto nb) {
-      // Block scale of this lane's 8 values: byte 2*fh + v/2 of the row's word.
-      const uint32_t sb = (r.s[nb] >> (16 * fh + 8 * (v / 2))) & 0xffu;
+    // Eight E2M1 values of packed word d times their E4M3 block scale (byte
+    // 2*fh + v/2 of the row's scale word), exact in binary16.
+    auto fp4x8 = [&](uint32_t d, uint32_t sword) {
+      const uint32_t sb = (sword >> (16 * fh + 8 * (v / 2))) & 0xffu;
       const v2h sc = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(sb | (sb << 8), 1.0f, false);
-      const uint32_t d = (uint32_t)r.w[nb][(int)v];
       const v2h y0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.0f, 0) * sc;
       const v2h y1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.0f, 1) * sc;
       const v2h y2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.0f, 2) * sc;
       const v2h y3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.0f, 3) * sc;
-      xw[nb] = v8h{y0[0], y0[1], y1[0], y1[1], y2[0], y2[1], y3[0], y3[1]};
+      return v8h{y0[0], y0[1], y1[0], y1[1], y2[0], y2[1], y3[0], y3[1]};
+    };
+    static_for<MB>([&](auto mb) {
+      if constexpr (A4) {
+        xa[mb] = fp4x8((uint32_t)r.a[mb][0][(int)v], r.as[mb]);
+      } else {
+        const uint32_t d0 = (uint32_t)r.a[mb][v / 2][(v % 2) * 2];
+        const uint32_t d1 = (uint32_t)r.a[mb][v / 2][(v % 2) * 2 + 1];
+        const v2h x0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, false);
+        const v2h x1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, true);
+        const v2h x2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, false);
+        const v2h x3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, true);
+        xa[mb] = v8h{x0[0], x0[1], x1[0], x1[1], x2[0], x2[1], x3[0], x3[1]};
+      }
     });
+    static_for<NB>([&](auto nb) { xw[nb] = fp4x8((uint32_t)r.w[nb][(int)v], r.s[nb]); });
     static_for<NB>([&](auto nb) {
       static_for<MB>([&](auto mb) {
         acc[nb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xw[nb], xa[mb], acc[nb][mb], 0, 0, 0);
@@ -422,7 +465,7 @@ hipError_t launch_nvfp4_gemm(const Fp4Params& p, int tile, hipStream_t s) {
     g.ldo = p.ldo;
     g.group_m = p.group_m;
     const int64_t tiles = ((p.m + 255) / 256) * ((p.n + 255) / 256);
-    nvfp4_gemm_pipe<<<dim3((unsigned)tiles), dim3(256), 0, s>>>(g);
+    nvfp4_gemm_pipe<false><<<dim3((unsigned)tiles), dim3(256), 0, s>>>(g);
     return hipGetLastError();
   }
   switch (tile) {
@@ -431,6 +474,32 @@ hipError_t launch_nvfp4_gemm(const Fp4Params& p, int tile, hipStream_t s) {
     case 3: return go(I64{}, I128{});
     default: return go(I128{}, I128{});
   }
+}
+
+hipError_t launch_nvfp4_w4a4(const uint8_t* a, int64_t lda, const uint8_t* as, const uint8_t* w,
+                             const uint8_t* ws, const float* alpha, int64_t m, int64_t n, int64_t k,
+                             const uint16_t* bias, uint16_t* out, int64_t ldo, int group_m,
+                             hipStream_t s) {
+  GemmParams g{};
+  g.a = a;
+  g.sa = nullptr;  // no per-row scale: the epilogue's row factor is 1
+  g.lda = lda;
+  g.asb = as;
+  g.w = w;
+  g.ldw = k / 2;
+  g.wsb = ws;
+  g.sw = alpha;
+  g.sw_step = 0;
+  g.m = m;
+  g.n = n;
+  g.k = k;
+  g.bias = bias;
+  g.out = out;
+  g.ldo = ldo;
+  g.group_m = group_m;
+  const int64_t tiles = ((m + 255) / 256) * ((n + 255) / 256);
+  nvfp4_gemm_pipe<true><<<dim3((unsigned)tiles), dim3(256), 0, s>>>(g);
+  return hipGetLastError();
 }
 
 hipError_t launch_nvfp4(const uint8_t* a, const float* sa, int64_t lda, const uint8_t* w,

@@ -327,3 +327,55 @@ def nvfp4_gemm(codes, act_scale, packed, block_scales, alpha, rows, bias=None):
              ptr(block_scales), ptr(alpha), rows, n, k, ptr(bias), ptr(out), out.stride(0),
              stream_of(device))
     return out
+
+
+def nvfp4_quantize_rows(matrix, global_sf):
+    """NVFP4 activation quantization (the W4A4 input).
+
+    ``matrix`` is bf16 or f16 ``[M, K]`` (K % 64 == 0, unit column stride),
+    ``global_sf`` an fp32 scalar tensor on the same device.  Returns packed E2M1
+    codes ``[M, K/2]`` (uint8) and E4M3 block scales ``[ceil128(M), K/16]``
+    (uint8, 128x4 order, padding rows 0).
+    """
+    if matrix.dtype not in (torch.bfloat16, torch.float16) or matrix.ndim != 2 or matrix.stride(1) != 1:
+        raise ValueError("NVFP4 quantization requires a 2-D BF16/F16 matrix with unit column stride")
+    if global_sf.dtype != torch.float32 or global_sf.numel() != 1:
+        raise ValueError("the NVFP4 global scale must be an fp32 scalar tensor")
+    m, k = matrix.shape
+    if k % 64:
+        raise ValueError("NVFP4 quantization needs K % 64 == 0")
+    device = require_device(matrix, global_sf)
+    m_pad = (m + 127) // 128 * 128
+    codes = torch.empty((m, k // 2), device=device, dtype=torch.uint8)
+    scales = torch.empty((m_pad, k // 16), device=device, dtype=torch.uint8)
+    if m:
+        call("vflash_nvfp4_quantize_rows", ptr(matrix), int(matrix.dtype == torch.float16), m, k,
+             matrix.stride(0), ptr(global_sf), ptr(codes), codes.stride(0), ptr(scales), m_pad,
+             stream_of(device))
+    return codes, scales
+
+
+def nvfp4_w4a4_gemm(codes, act_scales, packed, block_scales, alpha, rows, bias=None):
+    """W4A4 NVFP4 GEMM: out[rows, N] = bf16(bf16(alpha * a . w^T) + bias)."""
+    if codes.dtype != torch.uint8 or codes.ndim != 2 or codes.stride(1) != 1:
+        raise ValueError("NVFP4 activation codes must be a 2-D uint8 matrix")
+    if packed.dtype != torch.uint8 or block_scales.dtype != torch.uint8 or act_scales.dtype != torch.uint8:
+        raise ValueError("NVFP4 codes and block scales must be uint8")
+    n, half_k = packed.shape
+    k = 2 * half_k
+    if codes.shape != (rows, half_k):
+        raise ValueError("NVFP4 activation width differs from the weight")
+    if act_scales.shape != ((rows + 127) // 128 * 128, k // 16) or not act_scales.is_contiguous():
+        raise ValueError("NVFP4 activation scales must be the padded 128x4 layout")
+    if alpha.dtype != torch.float32 or alpha.numel() != 1:
+        raise ValueError("NVFP4 alpha must be an fp32 scalar tensor")
+    if bias is not None and (bias.dtype != torch.bfloat16 or bias.shape != (n,) or not bias.is_contiguous()):
+        raise ValueError("NVFP4 bias must be a contiguous BF16 vector of the output width")
+    device = require_device(codes, act_scales, packed, block_scales, alpha,
+                            *([bias] if bias is not None else []))
+    out = torch.empty((rows, n), device=device, dtype=torch.bfloat16)
+    if rows:
+        call("vflash_nvfp4_w4a4_linear", ptr(codes), codes.stride(0), ptr(act_scales), ptr(packed),
+             ptr(block_scales), ptr(alpha), rows, n, k, ptr(bias), ptr(out), out.stride(0),
+             stream_of(device))
+    return out

@@ -1,4 +1,4 @@
-"""NVFP4 block-scaled-weight linear on MI355X (drop-in for the reference module).
+"""NVFP4 linear on MI355X (drop-in for the reference module).
 
 Mirrors ``NVFP4Weight`` / ``NVFP4Execution`` of the reference
 (src/vflash/native/h3_nvfp4_linear.py:15-139): same packed-weight contract
@@ -6,12 +6,18 @@ Mirrors ``NVFP4Weight`` / ``NVFP4Execution`` of the reference
 128x4 tiled order, fp32 scalar ``alpha`` and ``input_scale``), same validation
 messages, counters (``calls``, ``rows``), inference-only rule and bias rule.
 
-Arithmetic (W4A8): activations are quantized per token to E4M3 by the same
-kernel as the FP8 path (``input_scale`` is validated and carried but only the
-W4A4 activation quantizer of the reference uses it); the GEMM multiplies E4M3
-activations by E2M1 weights times their E4M3 block scale, accumulates in
-binary32 and applies ``sa[m] * alpha`` in the epilogue, then the bias with a
-second bf16 rounding (h3_nvfp4_linear.py:139).
+Arithmetic (default, W4A4, the reference's): activations are quantized to
+NVFP4 with the weight's ``input_scale`` as the global scale (the contract of
+FlashInfer's ``nvfp4_quantize``, h3_nvfp4_linear.py:102), the GEMM multiplies
+E2M1 activations and weights, each times its E4M3 block scale (exact in
+binary16, binary32 accumulation), scales by ``alpha / input_scale`` and rounds
+to bf16, and the bias is added with a second bf16 rounding
+(h3_nvfp4_linear.py:114-139).
+
+``NVFP4Execution(activations="e4m3")`` selects W4A8 instead: per-token E4M3
+activations (the FP8 path's quantizer) times the same weights, ``sa[m] *
+alpha`` in the epilogue; ``input_scale`` is then not used.  It is the more
+accurate arithmetic, not the reference's.
 """
 
 from __future__ import annotations
@@ -69,11 +75,16 @@ def _require_device(device):
 
 
 class NVFP4Execution:
-    """W4A8 NVFP4-weight execution on gfx950; host counters remain diagnostic."""
+    """NVFP4 execution on gfx950 (W4A4 by default); host counters remain diagnostic."""
 
-    contract = "nvfp4-e2m1-block16-128x4-w4a8-gfx950-v1"
+    contract = "nvfp4-e2m1-block16-128x4-w4a4-gfx950-v1"
 
-    def __init__(self):
+    def __init__(self, activations: str = "nvfp4"):
+        if activations not in ("nvfp4", "e4m3"):
+            raise ValueError("NVFP4 activations are 'nvfp4' (W4A4) or 'e4m3' (W4A8)")
+        self.activations = activations
+        if activations == "e4m3":
+            self.contract = "nvfp4-e2m1-block16-128x4-w4a8-gfx950-v1"
         self.calls = 0
         self.rows = 0
 
@@ -94,19 +105,29 @@ class NVFP4Execution:
             or bias.dtype != torch.bfloat16
         ):
             raise ValueError("NVFP4 bias must match its BF16 output")
-        if values.dtype == torch.float16:
+        if self.activations == "e4m3" and values.dtype == torch.float16:
             raise ValueError("the W4A8 NVFP4 path quantizes BF16 (or FP32) activations")
         shape = values.shape
         matrix = values.to(torch.bfloat16) if values.dtype == torch.float32 else values
         matrix = matrix.reshape(-1, weight.in_features)
         if matrix.shape[0] == 0:
             raise ValueError("NVFP4 input rows must be nonempty")
-        if matrix.stride(1) != 1:
+        if matrix.stride(1) != 1 or matrix.stride(0) % 8:
             matrix = matrix.contiguous()
-        codes, act_scale = kernels.quantize_rows(matrix)
-        output = kernels.nvfp4_gemm(
-            codes, act_scale, weight.packed, weight.scales, weight.alpha, matrix.shape[0], bias
-        )
+        if self.activations == "nvfp4":
+            if matrix.data_ptr() % 16:
+                matrix = matrix.clone()  # the quantizer reads 16-byte vectors
+            codes, scales = kernels.nvfp4_quantize_rows(matrix, weight.input_scale)
+            # The output scale as the reference forms it (one fp32 division on the device).
+            alpha = weight.alpha / weight.input_scale
+            output = kernels.nvfp4_w4a4_gemm(
+                codes, scales, weight.packed, weight.scales, alpha, matrix.shape[0], bias
+            )
+        else:
+            codes, act_scale = kernels.quantize_rows(matrix)
+            output = kernels.nvfp4_gemm(
+                codes, act_scale, weight.packed, weight.scales, weight.alpha, matrix.shape[0], bias
+            )
         self.calls += 1
         self.rows += matrix.shape[0]
         return output.reshape(*shape[:-1], weight.out_features)

@@ -38,7 +38,8 @@ def quantize_weight_rows(weight: torch.Tensor):
 
 
 def e2m1_codes(values: torch.Tensor) -> torch.Tensor:
-    """Round binary32 values (already within [-6, 6]) to E2M1 codes, ties to even."""
+    """Round binary32 values (already within [-6, 6]) to E2M1 codes, ties to even;
+    the sign bit follows the input's sign, -0 included."""
     a = values.abs()
     code = (
         (a > 0.25).to(torch.uint8)
@@ -49,7 +50,7 @@ def e2m1_codes(values: torch.Tensor) -> torch.Tensor:
         + (a >= 3.5).to(torch.uint8)
         + (a > 5.0).to(torch.uint8)
     )
-    return code | ((values < 0).to(torch.uint8) << 3)
+    return code | (torch.signbit(values).to(torch.uint8) << 3)
 
 
 def scale_offsets_128x4(n: int, k_blocks: int, device=None) -> torch.Tensor:
