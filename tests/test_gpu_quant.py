@@ -181,3 +181,78 @@ def test_fast_row_division_gives_the_ieee_codes_on_every_bf16_pair(dev):
     fields = result.stdout.split()
     assert fields[0] == "pairs" and int(fields[1]) == fast_division_pairs(), result.stdout
     assert fields[2] == "code_mismatches" and int(fields[3]) == 0, result.stdout
+
+
+def non_finite_rows(k, seed=0):
+    """Rows holding NaN, -NaN, +-inf, an all-NaN row, and finite rows around them."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((8, k), generator=g).to(torch.bfloat16)
+    x[0, 3], x[0, 10] = float("nan"), 1000.0
+    x[1, 5], x[1, 6] = float("inf"), -0.0
+    x[2, 7], x[2, 9] = -float("inf"), float("inf")
+    x[3, :] = float("nan")
+    x[4, 0] = -float("nan")
+    x[5, 1], x[5, 2] = float("nan"), float("inf")
+    return x
+
+
+def assert_codes_like_torch(codes, scales, x):
+    """Bit-exact against the oracle (torch's arithmetic), except that every NaN
+    code may carry either sign: the host computes inf/inf as a negative NaN,
+    the GPU (like the reference's) as a positive one."""
+    rc, rs = O.quantize_rows(x.float().numpy())
+    c = codes.view(torch.uint8).cpu().numpy()
+    s = scales.reshape(-1).cpu().numpy()
+    assert np.array_equal(s.view(np.uint32), rs.view(np.uint32))
+    nan_ref = (rc & 0x7F) == 0x7F
+    assert np.array_equal((c & 0x7F) == 0x7F, nan_ref)
+    assert np.array_equal(c[~nan_ref], rc[~nan_ref])
+
+
+@pytest.mark.parametrize("k", [512, 5120, 200])
+def test_non_finite_rows_follow_torch(dev, k):
+    # torch's amax propagates NaN (scale 1), an infinite row gets scale inf
+    # (finite values -> signed zeros, inf/inf -> NaN), and clamp keeps NaN:
+    # _quantize_activation_torch (h3_fp8_linear.py:18-31) on such rows.
+    x = non_finite_rows(k)
+    codes, scales = kernels.quantize_rows(x.to(dev))  # k = 200: the generic kernel
+    assert_codes_like_torch(codes, scales, x)
+    if k % 16 == 0:
+        ref_c, ref_s = _quantize_activation_torch(x.to(dev))
+        assert torch.equal(scales, ref_s)
+
+
+def test_non_finite_rows_in_the_fused_quantizers(dev):
+    from vflash_amd.producers import rmsnorm_modulate_quantize
+
+    x = non_finite_rows(512, seed=1)
+    la = (torch.randn((32, 512)) * 0.05).to(torch.bfloat16)
+    codes, scales, _ = kernels.quantize_rows_lora(x.to(dev), la.to(dev))
+    assert_codes_like_torch(codes, scales, x)
+    # A NaN or inf anywhere in a row makes its RMSNorm all NaN (or NaN/zeros),
+    # which the producer quantizes with the same rules.
+    s = torch.zeros((8, 512), dtype=torch.bfloat16)
+    q = rmsnorm_modulate_quantize(x.reshape(1, 8, 512).to(dev), None, s.to(dev), s.to(dev), eps=1e-6,
+                                  keep_values=True)
+    assert_codes_like_torch(q.codes, q.scales, q.values.reshape(8, 512).cpu())
+    n = O.rms_norm(x.float().numpy(), None, 1e-6)
+    got = q.values.reshape(8, 512).float().cpu().numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(n))
+
+
+def test_requantization_after_a_nan_row(dev):
+    # A NaN input row makes the whole GELU output row NaN; its requantization
+    # must give NaN codes with scale 1 (torch's amax), not finite codes.
+    from vflash_amd.prepare import quantize_weight_rows
+
+    m, h, f = 32, 256, 512
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn((m, h), generator=g).to(torch.bfloat16)
+    x[5, 7] = float("nan")
+    cu, su = quantize_weight_rows(torch.randn((f, h), generator=g) * 0.02)
+    a, sa = kernels.quantize_rows(x.to(dev))
+    gg, amax = kernels.fp8_gemm_gelu(a, sa, cu.to(dev), su.to(dev), m)
+    assert torch.isnan(amax[5]).all() and not torch.isnan(amax[torch.arange(m) != 5]).any()
+    hc, hs = kernels.requant_rows(gg, amax)
+    assert_codes_like_torch(hc, hs, gg.cpu())
+    assert hs[5].item() == 1.0

@@ -160,6 +160,34 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Row maxima with NaN propagated, as torch's amax does: the bit patterns of
+// |x| (sign cleared) order like |x| with every NaN above infinity, so an
+// unsigned maximum of patterns is the maximum of |x|, or NaN when any x is NaN.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// acc (two 16-bit |bf16| patterns) updated with the two bf16 of word w.
+__device__ __forceinline__ uint32_t abs_max_pk(uint32_t acc, uint32_t w) {
+  const u16x2 a = __builtin_bit_cast(u16x2, acc), b = __builtin_bit_cast(u16x2, w & 0x7fff7fffu);
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(a, b));
+}
+
+// binary32 value of the larger of the two halves of abs_max_pk's accumulator.
+__device__ __forceinline__ float abs_max_value(uint32_t acc) {
+  return __uint_as_float(max(acc & 0xffffu, acc >> 16) << 16);
+}
+
+// Maximum of two non-negative binary32 values (NaN with the sign cleared included).
+__device__ __forceinline__ float nan_max(float a, float b) {
+  return __uint_as_float(max(__float_as_uint(a), __float_as_uint(b)));
+}
+
+__device__ __forceinline__ float wave_nan_max(float v) {
+  uint32_t u = __float_as_uint(v);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) u = max(u, (uint32_t)__shfl_xor((int)u, o, 64));
+  return __uint_as_float(u);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

@@ -148,8 +148,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
   const uint16_t* __restrict__ bias_p = p.bias;
 
   constexpr int NG = NB / 2 > 0 ? NB / 2 : 1;  // 64-column groups per wave (GELU maxima)
-  float rmax[MB][NG];
-  static_for<MB>([&](auto i) { static_for<NG>([&](auto j) { rmax[i][j] = 0.0f; }); });
+  // |g| maxima per (row block, 64-column group), NaN propagated (abs_max_pk).
+  uint32_t rmax[MB][NG];
+  static_for<MB>([&](auto i) { static_for<NG>([&](auto j) { rmax[i][j] = 0u; }); });
   float sam[MB];
   static_for<MB>([&](auto mb) {
     const int row = wm * WM + mb * 32 + fr;
@@ -222,8 +223,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
               pw = pack_bf16x2(bf16_lo(pw) + bv[g][i0], bf16_hi(pw) + bv[g][i1]);
             if constexpr (EPI == EPI_GELU) {
               pw = pack_bf16x2(gelu_tanh(bf16_lo(pw)), gelu_tanh(bf16_hi(pw)));
-              rmax[mb][nb / 2] =
-                  fmaxf(rmax[mb][nb / 2], fmaxf(fabsf(bf16_lo(pw)), fabsf(bf16_hi(pw))));
+              rmax[mb][nb / 2] = abs_max_pk(rmax[mb][nb / 2], pw);
             } else if constexpr (EPI == EPI_LORA) {
               uint32_t dp = pack_bf16x2(d[g * 4 + i0], d[g * 4 + i1]);
               if (p.lora_scale != 1.0f)
@@ -254,7 +254,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
     static_for<MB>([&](auto mb) {
       const int64_t m = m0 + wm * WM + mb * 32 + fr;
       static_for<NB / 2>([&](auto gi) {
-        const float v = fmaxf(rmax[mb][gi], __shfl_xor(rmax[mb][gi], 32, 64));
+        const float r = abs_max_value(rmax[mb][gi]);
+        const float v = nan_max(r, __uint_as_float((uint32_t)__shfl_xor((int)__float_as_uint(r), 32, 64)));
         const int64_t col = n0 + wn * WN + gi * 64;
         if (fh == 0 && m < p.m && col < p.n) p.amax_part[m * parts + col / 64] = v;
       });
@@ -284,7 +285,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
       const v4i vv = *reinterpret_cast<const v4i*>(stage + row * PITCH + ((c ^ rs) << 4));
       const v4i gg = *reinterpret_cast<const v4i*>(stage + row * PITCH + (((c + CHO) ^ rs) << 4));
       v4i h;
-      float amax = 0.0f;
+      uint32_t amax_pk = 0u;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t vw = (uint32_t)vv[j], gw = (uint32_t)gg[j];
@@ -292,11 +293,14 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
         const uint32_t sp = pack_bf16x2(g0 * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g0 * nlog2e)),
                                         g1 * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g1 * nlog2e)));
         const uint32_t hw = pack_bf16x2(bf16_lo(vw) * bf16_lo(sp), bf16_hi(vw) * bf16_hi(sp));
-        amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(hw)), fabsf(bf16_hi(hw))));
+        amax_pk = abs_max_pk(amax_pk, hw);
         h[j] = (int)hw;
       }
+      // Maximum over the 16 lanes of the 128-column group, NaN propagated.
+      uint32_t au = __float_as_uint(abs_max_value(amax_pk));
 #pragma unroll
-      for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+      for (int o = 8; o > 0; o >>= 1) au = max(au, (uint32_t)__shfl_xor((int)au, o, 64));
+      const float amax = __uint_as_float(au);
       if (valid) {
         const int64_t m = m0 + row;
         if (n < p.half_n) *reinterpret_cast<v4i*>(p.out + m * p.ldo + n) = h;

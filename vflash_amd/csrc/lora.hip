@@ -189,10 +189,10 @@ __global__ void __launch_bounds__(256) quant_lora_rows(
   // Quantization of the same registers (the arithmetic of quant_rows_vec).
   if (row < m_pad) {
     float amax = 0.0f;
-    static_for<QL_VPL>([&](auto i) { amax = fmaxf(amax, absmax8(v[i])); });
-    amax = wave_max(amax);
+    static_for<QL_VPL>([&](auto i) { amax = nan_max(amax, absmax8(v[i])); });
+    amax = wave_nan_max(amax);
     const float scale = row_scale(amax);
-    quant_row_regs<QL_VPL>(reinterpret_cast<uint2*>(codes + row * k), v, lane, nvec, scale);
+    quant_row_regs<QL_VPL>(reinterpret_cast<uint2*>(codes + row * k), v, lane, nvec, scale, amax);
     if (lane == 0) scales[row] = scale;
   }
 }

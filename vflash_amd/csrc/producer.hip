@@ -96,7 +96,7 @@ __global__ void __launch_bounds__(256) norm_mod_quant_rows(NormModParams p) {
   ss = wave_sum(ss);
   const float rstd = 1.0f / sqrtf(ss / (float)p.k + p.eps);
 
-  float amax = 0.0f;
+  uint32_t amax_pk = 0u;  // |y| maxima of the two halves, NaN propagated
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int j = lane + 64 * i;
@@ -108,11 +108,11 @@ __global__ void __launch_bounds__(256) norm_mod_quant_rows(NormModParams p) {
     for (int e = 0; e < 4; ++e) {
       const uint32_t y = modulate2<HAS_W>((uint32_t)v[i][e], (uint32_t)w[e], (uint32_t)s[e],
                                           (uint32_t)h[e], rstd);
-      amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(y)), fabsf(bf16_hi(y))));
+      amax_pk = abs_max_pk(amax_pk, y);
       v[i][e] = (int)y;
     }
   }
-  amax = wave_max(amax);
+  const float amax = wave_nan_max(abs_max_value(amax_pk));
   const float scale = row_scale(amax);
   if (p.values) {
     v4i* vr = reinterpret_cast<v4i*>(p.values + row * p.ldv);
@@ -122,7 +122,7 @@ __global__ void __launch_bounds__(256) norm_mod_quant_rows(NormModParams p) {
       if (j < nvec) vr[j] = v[i];
     }
   }
-  quant_row_regs<VPL>(cr, v, lane, nvec, scale);
+  quant_row_regs<VPL>(cr, v, lane, nvec, scale, amax);
   if (lane == 0) p.scales[row] = scale;
 }
 

@@ -2,7 +2,7 @@
 //
 // Arithmetic (reference: src/vflash/native/h3_fp8_activation.py:12-28 and its
 // portable twin src/vflash/native/h3_fp8_linear.py:18-31):
-//   amax  = max_k |x[row, k]|                       (binary32)
+//   amax  = max_k |x[row, k]|, NaN if any x is NaN  (binary32, torch's amax)
 //   scale = amax > 0 ? max(amax / 448, FLT_MIN) : 1 (IEEE division)
 //   code  = E4M3(clamp(x / scale, -448, 448))       (IEEE division, RNE)
 // Rows in [m, m_pad) are the GEMM padding rows: codes 0, scale 1.
@@ -46,12 +46,12 @@ __global__ void __launch_bounds__(256) quant_rows_vec(const uint16_t* __restrict
     int j = lane + 64 * i;
     if (j < nvec) {
       v[i] = __builtin_nontemporal_load(xr + j);
-      amax = fmaxf(amax, absmax8(v[i]));
+      amax = nan_max(amax, absmax8(v[i]));
     }
   }
-  amax = wave_max(amax);
+  amax = wave_nan_max(amax);
   const float scale = row_scale(amax);
-  quant_row_regs<VPL>(reinterpret_cast<uint2*>(codes + row * k), v, lane, nvec, scale);
+  quant_row_regs<VPL>(reinterpret_cast<uint2*>(codes + row * k), v, lane, nvec, scale, amax);
   if (lane == 0) scales[row] = scale;
 }
 
@@ -70,8 +70,8 @@ __global__ void __launch_bounds__(256) quant_rows_generic(const uint16_t* __rest
   }
   const uint16_t* xr = x + row * ldx;
   float amax = 0.0f;
-  for (int64_t j = lane; j < k; j += 64) amax = fmaxf(amax, fabsf(bf16_to_f32(xr[j])));
-  amax = wave_max(amax);
+  for (int64_t j = lane; j < k; j += 64) amax = nan_max(amax, bf16_to_f32(xr[j] & 0x7fffu));
+  amax = wave_nan_max(amax);
   const float scale = row_scale(amax);
   uint8_t* cr = codes + row * k;
   for (int64_t j = lane; j < k; j += 64) cr[j] = (uint8_t)quant1(bf16_to_f32(xr[j]), scale);
@@ -95,13 +95,13 @@ __global__ void __launch_bounds__(256) requant_rows(const uint16_t* __restrict__
     return;
   }
   float amax = 0.0f;
-  for (int p = lane; p < parts; p += 64) amax = fmaxf(amax, amax_part[row * parts + p]);
-  amax = wave_max(amax);
+  for (int p = lane; p < parts; p += 64) amax = nan_max(amax, amax_part[row * parts + p]);
+  amax = wave_nan_max(amax);
   const float scale = row_scale(amax);
   const v4i* gr = reinterpret_cast<const v4i*>(g + row * ldg);
   uint2* cr = reinterpret_cast<uint2*>(codes + row * k);
   const int nvec = (int)(k >> 3);
-  const RowDivisor d = row_divisor(scale);
+  const RowDivisor d = row_divisor(scale, amax);
   if (d.fast) {
     for (int j = lane; j < nvec; j += 64) cr[j] = quant8<true>(__builtin_nontemporal_load(gr + j), d);
   } else {

@@ -6,27 +6,27 @@
 
 namespace vfa {
 
+// max |x| over 8 bf16 values (one 16-byte vector), NaN propagated (abs_max_pk).
 __device__ __forceinline__ float absmax8(v4i v) {
-  float m = 0.0f;
+  uint32_t acc = 0u;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint32_t w = (uint32_t)v[j];
-    m = fmaxf(m, fabsf(bf16_to_f32(w & 0xffffu)));
-    m = fmaxf(m, fabsf(bf16_to_f32(w >> 16)));
-  }
-  return m;
+  for (int j = 0; j < 4; ++j) acc = abs_max_pk(acc, (uint32_t)v[j]);
+  return abs_max_value(acc);
 }
 
+// amax > 0 ? max(amax / 448, FLT_MIN) : 1.  A NaN maximum gives 1 (NaN > 0 is
+// false) and an infinite one gives infinity, as the reference's torch.where does.
 __device__ __forceinline__ float row_scale(float amax) {
   return amax > 0.0f ? fmaxf(amax / 448.0f, VFA_FLT_MIN) : 1.0f;
 }
 
-__device__ __forceinline__ float clamped_quotient(float x, float scale) {
-  return fminf(fmaxf(x / scale, -448.0f), 448.0f);
+// clamp(q, -448, 448) with NaN kept (torch.clamp), for rows that may hold NaN.
+__device__ __forceinline__ float clamp448_keep_nan(float q) {
+  return q != q ? q : fminf(fmaxf(q, -448.0f), 448.0f);
 }
 
 __device__ __forceinline__ uint32_t quant1(float x, float scale) {
-  return f32_to_e4m3(clamped_quotient(x, scale));
+  return f32_to_e4m3(clamp448_keep_nan(x / scale));
 }
 
 // Division of a row by its scale.
@@ -48,14 +48,19 @@ __device__ __forceinline__ uint32_t quant1(float x, float scale) {
 // tests/probes/row_division.hip repeats the comparison on the GPU.
 struct RowDivisor {
   float s, y;
-  bool fast;  // uniform over the wave: the scale must be
+  bool fast;  // uniform over the wave: the scale and the row maximum must be
 };
 
-__device__ __forceinline__ RowDivisor row_divisor(float s) {
+// Rows whose maximum is NaN or infinite take the exact path, where the clamp
+// keeps NaN and the software encoder gives it the NaN code (the reference's
+// torch.clamp and float8 cast); every finite row with a scale in range takes
+// the fast path, where no x can be NaN.
+__device__ __forceinline__ RowDivisor row_divisor(float s, float amax) {
   RowDivisor d;
   d.s = s;
   d.y = 1.0f / s;
-  d.fast = __builtin_amdgcn_readfirstlane((s >= 0x1p-72f && s <= 3.40282347e38f) ? 1 : 0) != 0;
+  const bool fast = amax <= 3.40282347e38f && s >= 0x1p-72f && s <= 3.40282347e38f;
+  d.fast = __builtin_amdgcn_readfirstlane(fast ? 1 : 0) != 0;
   return d;
 }
 
@@ -72,7 +77,8 @@ __device__ __forceinline__ float row_quotient(float x, const RowDivisor& d) {
 
 template <bool FAST>
 __device__ __forceinline__ float clamped_row_quotient(float x, const RowDivisor& d) {
-  return fminf(fmaxf(row_quotient<FAST>(x, d), -448.0f), 448.0f);
+  if constexpr (FAST) return fminf(fmaxf(row_quotient<true>(x, d), -448.0f), 448.0f);
+  return clamp448_keep_nan(row_quotient<false>(x, d));
 }
 
 // 8 bf16 values (one 16-byte vector) -> 8 E4M3 codes packed little-endian.
@@ -82,6 +88,18 @@ __device__ __forceinline__ float clamped_row_quotient(float x, const RowDivisor&
 // |x| <= 448, both signs, found no difference.
 template <bool FAST>
 __device__ __forceinline__ uint2 quant8(v4i v, const RowDivisor& d) {
+  if constexpr (!FAST) {
+    // Exact path: IEEE division, NaN kept, software encoder (NaN -> 0x7f | sign).
+    uint32_t c[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t w = (uint32_t)v[j];
+      c[2 * j] = f32_to_e4m3(clamped_row_quotient<false>(bf16_lo(w), d));
+      c[2 * j + 1] = f32_to_e4m3(clamped_row_quotient<false>(bf16_hi(w), d));
+    }
+    return make_uint2(c[0] | c[1] << 8 | c[2] << 16 | c[3] << 24,
+                      c[4] | c[5] << 8 | c[6] << 16 | c[7] << 24);
+  }
   float q[8];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -103,8 +121,8 @@ __device__ __forceinline__ uint2 quant8(v4i v, const RowDivisor& d) {
 // vector lane + 64 i of the row (i < VPL, lane + 64 i < nvec).
 template <int VPL>
 __device__ __forceinline__ void quant_row_regs(uint2* cr, const v4i (&v)[VPL], int lane, int nvec,
-                                               float scale) {
-  const RowDivisor d = row_divisor(scale);
+                                               float scale, float amax) {
+  const RowDivisor d = row_divisor(scale, amax);
   if (d.fast) {
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
