@@ -11,8 +11,8 @@ HBM.  A step is one ``linear`` call; K timed steps are bracketed by
 events recorded on the launch stream around each of its launches in the timed
 region.  Prints one JSON line.
 
-Other workloads (``qkv``, ``ffn``, ``ffn_swiglu``, ``skinny``, ``nvfp4`` (W4A4),
-``nvfp4_w4a8``, ``small``, ``norm_quant``) print the same kind of line for the other shapes of this path; ``copy`` times a plain
+Other workloads (``qkv``, ``ffn``, ``ffn_swiglu``, ``skinny``, ``nvfp4`` (W4A8, as configured),
+``nvfp4_w4a4``, ``small``, ``norm_quant``) print the same kind of line for the other shapes of this path; ``copy`` times a plain
 1 GiB device copy, the calibration kernel for the HBM byte counters.  For the
 launch-bound shapes (``small``, ``skinny``) the line adds a device-side time
 per step measured with the launch queue filled ahead.
@@ -42,7 +42,7 @@ def parse():
     p.add_argument(
         "--workload",
         default="fp8_linear",
-        choices=["fp8_linear", "qkv", "ffn", "ffn_swiglu", "skinny", "nvfp4", "nvfp4_w4a8", "small",
+        choices=["fp8_linear", "qkv", "ffn", "ffn_swiglu", "skinny", "nvfp4", "nvfp4_w4a4", "small",
                  "norm_quant", "copy"],
     )
     p.add_argument("--skinny-m", type=int, default=1024)
@@ -333,14 +333,15 @@ def make_workload(args, dev):
              "operand_sets": count, "flops_per_step": 2.0 * m * n * k + 2.0 * m * r * (k + n)},
             launch_bound=True)
 
-    if wl in ("nvfp4", "nvfp4_w4a8"):
+    if wl in ("nvfp4", "nvfp4_w4a4"):
         from vflash_amd.nvfp4_linear import NVFP4Execution, NVFP4Weight
         from vflash_amd.prepare import quantize_nvfp4_weight
 
-        # W4A4 (the reference's arithmetic): NVFP4 activations with a calibrated
-        # global input scale (448 * 6 / amax), E2M1 weights with E4M3 block scales.
-        # nvfp4_w4a8: per-token E4M3 activations against the same weights.
-        w4a4 = wl == "nvfp4"
+        # nvfp4: the NVFP4-weight linear as its benchmark configuration states it,
+        # per-token E4M3 activations against E2M1 weights with E4M3 block scales
+        # (W4A8).  nvfp4_w4a4: the reference module's arithmetic, NVFP4 activations
+        # with a calibrated global input scale (448 * 6 / amax).
+        w4a4 = wl == "nvfp4_w4a4"
         m, k, n = 32760, 5120, 13824
         g = torch.Generator().manual_seed(0)
         x = torch.randn((m, k), generator=g).to(torch.bfloat16)
