@@ -285,7 +285,9 @@ int vflash_nvfp4_w4a4_linear(const void* a, int64_t lda, const void* a_scales, c
  * 12 = 128x128 two-slot pipeline, two workgroups per CU,
  * 13 / 14 = 128x128 with four / three stage slots,
  * 15 = tile 10 with the stage barrier after K-substep 0, 16 = tile 10 with
- * scalar-offset DMA, 17 = both (default for large shapes))
+ * scalar-offset DMA, 17 = both (default for large shapes), 18 = tile 12 with
+ * tile 17's schedule, 19 = tile 17 as a persistent grid whose epilogue stores
+ * from registers while the next tile's first stages load)
  * and the tile-order group height (0 = default).  For vflash_nvfp4_linear the
  * values mean 1 = 256x256, 2 = 128x128, 3 = 64x128 (register-staged) and
  * 4 = 256x256 pipelined (default for large shapes); other values select the

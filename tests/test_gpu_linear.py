@@ -12,7 +12,7 @@ from vflash_amd.prepare import quantize_weight_rows
 
 pytestmark = pytest.mark.gpu
 
-TILES = [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18]
+TILES = [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19]
 
 
 @pytest.fixture
@@ -126,3 +126,21 @@ def test_metric_shape_sampled_rows(dev):
     got = out.float().cpu().numpy()[rows]
     rel_check(got, oracle_linear(x, codes, scale, b, rows=rows))
     assert bool(torch.isfinite(out.float()).all())
+
+
+@pytest.mark.parametrize("m,k,n", [(4400, 128, 4112), (4400, 256, 4112), (5000, 640, 4096)])
+def test_persistent_tiles_with_several_tiles_per_workgroup(dev, tile, m, k, n):
+    # More 256x256 tiles than compute units, partial tiles on both edges, and
+    # K of one and two stages: every workgroup of tile 19 runs several tiles,
+    # each issuing the next one's first stages after its stores.
+    x, codes, scale, b = seeded(m, k, n, seed=k)
+    codes_d, scale_d = codes.to(dev), scale.to(dev)
+    a, sa = kernels.quantize_rows(x.to(dev))
+    _lib.set_gemm_tile(17)
+    ref = kernels.fp8_gemm(a, sa, codes_d, scale_d, m, b.to(dev))
+    _lib.set_gemm_tile(19)
+    out = kernels.fp8_gemm(a, sa, codes_d, scale_d, m, b.to(dev))
+    assert torch.equal(out, ref)  # same sum order per element, same epilogue arithmetic
+    out = kernels.fp8_gemm(a, sa, codes_d, scale_d, m, None)
+    rows = np.r_[0:8, m // 2: m // 2 + 8, m - 8:m]
+    rel_check(out.float().cpu().numpy()[rows], oracle_linear(x, codes, scale, None, rows))

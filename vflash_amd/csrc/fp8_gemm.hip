@@ -304,10 +304,21 @@ constexpr int PIPE2_LDS = pipe2_lds(256);  // two 64 KB stage slots
 // SDMA: K % 128 == 0; the DMA advances K through the scalar offset and kills
 // stages past the end by switching to an empty buffer resource, so issuing a
 // DMA instruction costs no vector instruction.
-template <int EPI, int BT = 256, int NS = 2, int PRE = -1, bool SDMA = false>
+// PERSIST (EPI_BIAS, 256x256, two slots, SDMA): one tile of a persistent
+// workgroup.  The epilogue stores straight from registers (direct_epilogue),
+// so the ring is free once the main loop ends: when `has_next`, the scale/bias
+// vectors of tile (tm2, tn2) (into the other vector buffer, vec_lds2) and its
+// stages 0 and 1 are issued before this tile's 32 stores per wave.  Vector
+// memory operations complete in issue order, so the next tile waits for stage
+// 0 with vmcnt <= DMA + 32 and for stage 1 with vmcnt <= 32, and the stores
+// drain behind its first MFMAs; `first` tiles issue their own vectors and
+// stages and wait as the non-persistent form does.
+template <int EPI, int BT = 256, int NS = 2, int PRE = -1, bool SDMA = false, bool PERSIST = false>
 __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, uint8_t* ring,
                                            uint32_t ring_lds, uint8_t* vec, uint32_t vec_lds,
-                                           int wave) {
+                                           int wave, bool first = true, bool has_next = false,
+                                           int tm2 = 0, int tn2 = 0, uint32_t vec_lds2 = 0) {
+  static_assert(!PERSIST || (EPI == EPI_BIAS && BT == 256 && NS == 2 && SDMA), "persistent form");
   constexpr int BM = BT, BN = BT, BK = 128, WGM = 2, WGN = 2;
   constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
   constexpr int HALF = BM * BK;            // one operand of one stage (32 KB at BT = 256)
@@ -453,9 +464,14 @@ __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, 
   constexpr bool LORA_PRE = EPI == EPI_LORA && BT == 128;
   v16f lora_d[LORA_PRE ? MB * NB : 1];
   if constexpr (LORA_PRE) lora_blocks<BM, BN, WGM, WGN>(p, m0, n0, wm, wn, lane, lora_d);
-  stage_vectors<BM, BN, EPI == EPI_SWIGLU>(p, m0, n0, wave, lane, vec_lds);
-  static_for<NS>([&](auto s) { issue((int)s, (int)s); });
-  wait_vmcnt<(NS - 1) * DMA, true>();
+  constexpr int STORES = PERSIST ? NB * MB * 2 : 0;  // direct_epilogue's stores per wave
+  if (!PERSIST || first) {
+    stage_vectors<BM, BN, EPI == EPI_SWIGLU>(p, m0, n0, wave, lane, vec_lds);
+    static_for<NS>([&](auto s) { issue((int)s, (int)s); });
+    wait_vmcnt<(NS - 1) * DMA, true>();
+  } else {
+    wait_vmcnt<(NS - 1) * DMA + STORES, true>();  // the previous tile's stores may drain
+  }
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   read(I0{}, I0{});
@@ -476,7 +492,10 @@ __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, 
     __builtin_amdgcn_sched_barrier(0);
     // Stage kt+1 has landed for every wave (the DMAs of stages kt+2 ..
     // kt+NS-1 may still be in flight); stage kt is fully read.
-    wait_vmcnt<(NS - 2) * DMA, true>();
+    if (PERSIST && kt == 0 && !first)
+      wait_vmcnt<(NS - 2) * DMA + STORES, true>();
+    else
+      wait_vmcnt<(NS - 2) * DMA, true>();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -508,8 +527,31 @@ __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, 
   wait_vmcnt<0, true>();  // every DMA has landed before the ring is reused
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  gemm_epilogue<BM, BN, WGM, WGN, EPI, true>(p, acc, m0, n0, wm, wn, tid_v, ring, vec,
-                                             LORA_PRE ? lora_d : nullptr);
+  if constexpr (PERSIST) {
+    // The ring is free since the barrier above; the other vector buffer was
+    // last read by the previous tile's epilogue, before this tile's barriers.
+    if (has_next) {
+      const int64_t m2 = (int64_t)tm2 * BM, n2 = (int64_t)tn2 * BN;
+      const int64_t ra_rows = min((int64_t)BM, p.m - m2), rw_rows = min((int64_t)BN, p.n - n2);
+      const SDma d0{make_rsrc(p.a + m2 * p.lda, (uint32_t)(ra_rows * p.lda)),
+                    make_rsrc(p.w + n2 * p.ldw, (uint32_t)(rw_rows * p.ldw)), wave_lds, 0u};
+      SDma d1 = d0;
+      d1.base = wave_lds + SLOT;
+      d1.kb = BK;
+      if (KT < 2) {  // one-stage K: the second slot loads nothing
+        d1.ra = ra_none;
+        d1.rw = rw_none;
+        d1.kb = 0u;
+      }
+      stage_vectors<BM, BN, false>(p, m2, n2, wave, lane, vec_lds2);
+      static_for<DMA>([&](auto i) { sdma_one(d0, i); });
+      static_for<DMA>([&](auto i) { sdma_one(d1, i); });
+    }
+    direct_epilogue<BM, BN, WGM, WGN>(p, acc, m0, n0, wm, wn, lane, vec);
+  } else {
+    gemm_epilogue<BM, BN, WGM, WGN, EPI, true>(p, acc, m0, n0, wm, wn, tid_v, ring, vec,
+                                               LORA_PRE ? lora_d : nullptr);
+  }
 }
 
 template <int EPI, int PRE = -1, bool SDMA = false>
@@ -576,6 +618,57 @@ __global__ void __launch_bounds__(256) fp8_gemm_persist(const GemmParams p) {
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   }
+}
+
+// Persistent 256x256 EPI_BIAS form with the direct-store epilogue: tile i's
+// stores drain while tile i+1's first stages load (tiles as fp8_gemm_persist
+// assigns them).
+template <int PRE>
+__global__ void __launch_bounds__(256) fp8_gemm_persist2(const GemmParams p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[PIPE2_LDS];
+  __shared__ __attribute__((aligned(1024))) uint8_t vec[2][VEC_LDS];  // alternate per tile
+  const int tiles_m = (int)((p.m + 255) / 256), tiles_n = (int)((p.n + 255) / 256);
+  const int T = tiles_m * tiles_n, G = gridDim.x, b = blockIdx.x;
+  int first, end, stride;
+  if (G >= 8 && (G & 7) == 0) {
+    const int x = b & 7, q = T >> 3, rem = T & 7;
+    first = x * q + min(x, rem) + (b >> 3);
+    end = x * q + min(x, rem) + q + (x < rem ? 1 : 0);
+    stride = G >> 3;
+  } else {
+    first = b;
+    end = T;
+    stride = G;
+  }
+  int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(ring));
+  uint32_t vec_lds = __builtin_amdgcn_readfirstlane(lds_addr(vec[0]));
+  asm volatile("" : "+s"(wave), "+s"(ring_lds), "+s"(vec_lds));
+  int tm, tn;
+  if (first < end) grouped_tile(first, tiles_m, tiles_n, p.group_m, tm, tn);
+  int cur = 0;
+  for (int logical = first; logical < end; logical += stride) {
+    const int next = logical + stride;
+    const bool has_next = next < end;
+    int tm2 = 0, tn2 = 0;
+    if (has_next) grouped_tile(next, tiles_m, tiles_n, p.group_m, tm2, tn2);
+    pipe2_tile<EPI_BIAS, 256, 2, PRE, true, true>(
+        p, tm, tn, ring, ring_lds, vec[cur], vec_lds + cur * VEC_LDS, wave, logical == first,
+        has_next, tm2, tn2, vec_lds + (1 - cur) * VEC_LDS);
+    tm = tm2;
+    tn = tn2;
+    cur = 1 - cur;
+  }
+}
+
+int compute_units();
+
+template <int PRE>
+static hipError_t launch_persist2(const GemmParams& p, hipStream_t s) {
+  const int64_t tiles = ((p.m + 255) / 256) * ((p.n + 255) / 256);
+  const int64_t grid = tiles < compute_units() ? tiles : compute_units();
+  fp8_gemm_persist2<PRE><<<dim3((unsigned)grid), dim3(256), 0, s>>>(p);
+  return hipGetLastError();
 }
 
 template <int EPI, int PRE = -1, bool SDMA = false>
@@ -661,6 +754,16 @@ hipError_t launch_epi(const GemmParams& p, int tile, hipStream_t s) {
     // Tile 12 with tile 17's schedule.
     case 18: return p.k % 128 ? launch_pipe2s<EPI, 2, 0, false>(p, s)
                               : launch_pipe2s<EPI, 2, 0, true>(p, s);
+    // Tile 17's schedule as a persistent grid whose epilogue stores from
+    // registers while the next tile loads (EPI_BIAS without planes, K % 128 == 0,
+    // 16-byte output rows); other cases run tile 17.
+    case 19:
+      if constexpr (EPI == EPI_BIAS) {
+        if (p.k % 128 == 0 && p.plane_cols == 0 && p.ldo % 8 == 0 &&
+            (reinterpret_cast<uintptr_t>(p.out) & 15) == 0 && 256 * p.ldo * 2 < (int64_t(1) << 31))
+          return launch_persist2<0>(p, s);
+      }
+      return p.k % 128 ? launch_pipe2<EPI, 0, false>(p, s) : launch_pipe2<EPI, 0, true>(p, s);
     default: return hipErrorInvalidValue;
   }
 }
