@@ -288,7 +288,8 @@ int vflash_nvfp4_w4a4_linear(const void* a, int64_t lda, const void* a_scales, c
  * scalar-offset DMA, 17 = both (default for large shapes), 18 = tile 12 with
  * tile 17's schedule, 19 = tile 17 as a persistent grid whose epilogue stores
  * from registers while the next tile's first stages load)
- * and the tile-order group height (0 = default).  For vflash_nvfp4_linear the
+ * and the tile-order group height (0 = default: 2 for the E4M3 GEMMs, 8 for the
+ * E2M1-weight ones).  For vflash_nvfp4_linear the
  * values mean 1 = 256x256, 2 = 128x128, 3 = 64x128 (register-staged) and
  * 4 = 256x256 pipelined (default for large shapes); other values select the
  * automatic choice there.  Returns the previous tile value.

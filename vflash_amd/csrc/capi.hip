@@ -34,7 +34,11 @@ hipError_t launch_nvfp4(const uint8_t*, const float*, int64_t, const uint8_t*, c
 namespace {
 
 int g_tile = 0;     // tuning override (0 = automatic)
-int g_group_m = 8;  // tile-order group height
+// Tile-order group height (0 = automatic: 2 for the E4M3 GEMMs and 8 for the
+// E2M1-weight GEMM, the fastest of a sweep over 1..32 at the large shapes).
+int g_group_m = 0;
+int fp8_group_m() { return g_group_m > 0 ? g_group_m : 2; }
+int fp4_group_m() { return g_group_m > 0 ? g_group_m : 8; }
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
@@ -73,7 +77,7 @@ vfa::GemmParams base_params(const void* a, const float* sa, int64_t lda, const v
   p.ldo = ldo;
   p.lora_scale = 1.0f;
   p.lora_strength = 1.0f;
-  p.group_m = g_group_m;
+  p.group_m = fp8_group_m();
   p.tile = g_tile;
   return p;
 }
@@ -96,7 +100,7 @@ const char* vflash_status_string(int s) {
 int vflash_set_gemm_tile(int tile, int group_m) {
   const int prev = g_tile;
   if (tile >= 0 && tile <= 19) g_tile = tile;
-  g_group_m = group_m > 0 ? group_m : 8;
+  g_group_m = group_m > 0 ? group_m : 0;
   return prev;
 }
 
@@ -306,7 +310,7 @@ int vflash_nvfp4_linear(const void* a, const float* sa, int64_t lda, const void*
                                   static_cast<const uint8_t*>(w_packed),
                                   static_cast<const uint8_t*>(w_scales), alpha, m, n, k,
                                   static_cast<const uint16_t*>(bias),
-                                  static_cast<uint16_t*>(out), ldo, tile, g_group_m,
+                                  static_cast<uint16_t*>(out), ldo, tile, fp4_group_m(),
                                   static_cast<hipStream_t>(stream)));
 }
 
@@ -338,7 +342,7 @@ int vflash_nvfp4_w4a4_linear(const void* a, int64_t lda, const void* a_scales, c
   return status(vfa::launch_nvfp4_w4a4(
       static_cast<const uint8_t*>(a), lda, static_cast<const uint8_t*>(a_scales),
       static_cast<const uint8_t*>(w_packed), static_cast<const uint8_t*>(w_scales), alpha, m, n, k,
-      static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(out), ldo, g_group_m,
+      static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(out), ldo, fp4_group_m(),
       static_cast<hipStream_t>(stream)));
 }
 
