@@ -22,7 +22,7 @@ def tile():
 
 
 def seeded(m, k, n, bias=True, seed=0):
-    """BASELINE input recipe: fp32 draws on CPU in the order X, W, bias, then casts."""
+    """The benchmark input recipe: fp32 draws on CPU in the order X, W, bias, then casts."""
     g = torch.Generator().manual_seed(seed)
     x = torch.randn((m, k), generator=g).to(torch.bfloat16)
     w = torch.randn((n, k), generator=g) * 0.02
@@ -56,7 +56,7 @@ def test_golden_small_case_through_the_c_abi(dev):
     rel_check(nob, g["scaled"])
 
 
-def test_baseline_config_small_linear(dev):
+def test_small_linear_4096x3072x3072(dev):
     # X bf16 [4096, 3072] N(0,1); W N(0, 0.02) -> e4m3 [3072, 3072]; bias N(0, 0.01); seed 0.
     x, codes, scale, b = seeded(4096, 3072, 3072)
     ex = RowFP8Execution("w8a8", activation_quantizer="triton")
