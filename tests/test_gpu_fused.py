@@ -229,9 +229,11 @@ def test_swiglu_h3_shape_sampled(dev):
     assert bool(torch.isfinite(hh.float()).all())
 
 
-@pytest.mark.parametrize("m,n", [(256, 1536), (512, 4608), (1024, 6144)])
+@pytest.mark.parametrize("m", [256, 512, 1024])
+@pytest.mark.parametrize("n", [1536, 4608, 6144])
 @pytest.mark.parametrize("scaling,strength", [(1.0, 1.0), (0.5, 1.375)])
 def test_lora_linear_skinny_shapes(dev, m, n, scaling, strength):
+    # Every skinny audio-stream shape: M in {256, 512, 1024} x N in {1536, 4608, 6144}, K 1536.
     k, r = 1536, 32
     g = torch.Generator().manual_seed(m + n)
     x = torch.randn((m, k), generator=g).to(torch.bfloat16)

@@ -25,23 +25,12 @@
 
 namespace vfa {
 
-__device__ __forceinline__ float sumsq8(v4i v) {
-  float s = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float a = bf16_lo((uint32_t)v[j]), b = bf16_hi((uint32_t)v[j]);
-    s += a * a;  // exact: a bf16 square has at most 16 significant bits
-    s += b * b;
-  }
-  return s;
-}
-
 // Norm and modulation of the two bf16 of one 32-bit word (low element first),
 // every rounding done for both at once; returns y as a packed bf16 pair.
 template <bool HAS_W>
-__device__ __forceinline__ uint32_t modulate2(uint32_t xv, uint32_t wv, uint32_t sv, uint32_t hv,
-                                              float rstd) {
-  float nl = bf16_lo(xv) * rstd, nh = bf16_hi(xv) * rstd;
+__device__ __forceinline__ uint32_t modulate2(float xl, float xh, uint32_t wv, uint32_t sv,
+                                              uint32_t hv, float rstd) {
+  float nl = xl * rstd, nh = xh * rstd;
   if constexpr (HAS_W) {
     nl *= bf16_lo(wv);
     nh *= bf16_hi(wv);
@@ -84,13 +73,22 @@ __global__ void __launch_bounds__(256) norm_mod_quant_rows(NormModParams p) {
   const v4i* sr = reinterpret_cast<const v4i*>(p.scale + mrow * p.ld_scale);
   const v4i* hr = reinterpret_cast<const v4i*>(p.shift + mrow * p.ld_shift);
   const v4i* wr = reinterpret_cast<const v4i*>(p.norm_w);
+  // x is widened to binary32 once (the second pass reuses it); v[] later holds y.
   v4i v[VPL];
+  float xf[VPL][8];
   float ss = 0.0f;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int j = lane + 64 * i;
-    v[i] = __builtin_nontemporal_load(xr + (j < nvec ? j : nvec - 1));
-    const float part = sumsq8(v[i]);
+    const v4i xv = __builtin_nontemporal_load(xr + (j < nvec ? j : nvec - 1));
+    float part = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      xf[i][2 * e] = bf16_lo((uint32_t)xv[e]);
+      xf[i][2 * e + 1] = bf16_hi((uint32_t)xv[e]);
+      part += xf[i][2 * e] * xf[i][2 * e];  // exact squares (16 significant bits)
+      part += xf[i][2 * e + 1] * xf[i][2 * e + 1];
+    }
     ss += j < nvec ? part : 0.0f;
   }
   ss = wave_sum(ss);
@@ -106,8 +104,8 @@ __global__ void __launch_bounds__(256) norm_mod_quant_rows(NormModParams p) {
     if constexpr (HAS_W) w = wr[jj];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const uint32_t y = modulate2<HAS_W>((uint32_t)v[i][e], (uint32_t)w[e], (uint32_t)s[e],
-                                          (uint32_t)h[e], rstd);
+      const uint32_t y = modulate2<HAS_W>(xf[i][2 * e], xf[i][2 * e + 1], (uint32_t)w[e],
+                                          (uint32_t)s[e], (uint32_t)h[e], rstd);
       amax_pk = abs_max_pk(amax_pk, y);
       v[i][e] = (int)y;
     }
