@@ -44,10 +44,14 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
   return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
-// Two binary32 values -> one packed bf16 pair (low half = a), RNE, one instruction.
+// Two binary32 values -> one packed bf16 pair (low half = a), RNE, one
+// v_cvt_pk_bf16_f32.  Written as an instruction the compiler keeps whole:
+// when the two halves of a pair are read back separately it would otherwise
+// convert each value on its own and re-extract it with shifts and masks.
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  const v2bf v = {(__bf16)a, (__bf16)b};
-  return __builtin_bit_cast(uint32_t, v);
+  uint32_t r;
+  asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
 }
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
