@@ -15,7 +15,8 @@ Other workloads (``qkv``, ``ffn``, ``ffn_swiglu``, ``skinny``, ``nvfp4`` (W4A8, 
 ``nvfp4_w4a4``, ``small``, ``norm_quant``) print the same kind of line for the other shapes of this path; ``copy`` times a plain
 1 GiB device copy, the calibration kernel for the HBM byte counters.  For the
 launch-bound shapes (``small``, ``skinny``) the line adds a device-side time
-per step measured with the launch queue filled ahead.
+per step measured with the launch queue filled ahead; ``skinny`` also adds the
+step rate when each step is replayed from a captured HIP graph.
 """
 
 from __future__ import annotations
@@ -163,6 +164,8 @@ class Workload:
         # launches, so device time is also measured with the queue filled ahead.
         self.launch_bound = launch_bound
         self.extra = None  # optional comparison timing: () -> ms per step
+        # Optional: () -> ms per step with the step replayed from captured HIP graphs.
+        self.graph = None
 
 
 def rate(work, ms, unit):
@@ -326,12 +329,39 @@ def make_workload(args, dev):
         step_bytes = (2 * m * k + 2 * m * k + 8 * m + n * k + 6 * n
                       + 2 * r * (k + n) + 4 * m * r + 2 * m * n)
         gemm_bytes = m * k + 4 * m + n * k + 6 * n + 2 * m * r + 2 * n * r + 2 * m * n
-        return Workload(
+
+        def graph_ms():
+            # The same step (both launches) captured once per operand set into a
+            # HIP graph and replayed: what a launch-bound caller does to skip the
+            # per-call host path.
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                step(0, None)
+            torch.cuda.current_stream().wait_stream(side)
+            graphs = []
+            for i in range(len(sets)):
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    step(i, None)
+                graphs.append(graph)
+            for i in range(2 * len(graphs)):
+                graphs[i % len(graphs)].replay()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for i in range(args.steps):
+                graphs[i % len(graphs)].replay()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) * 1e3 / args.steps
+
+        wlo = Workload(
             wl, f"Skinny-M FP8 linear + rank-32 LoRA GB/s (M={m},K={k},N={n})", "GB/s", step_bytes, step,
             "fp8_gemm_lora", gemm_bytes, "hbm", HBM_PEAK_GBS,
             {"workload": f"skinny_lora_m{m}_k{k}_n{n}_r{r}", "m": m, "k": k, "n": n, "rank": r,
              "operand_sets": count, "flops_per_step": 2.0 * m * n * k + 2.0 * m * r * (k + n)},
             launch_bound=True)
+        wlo.graph = graph_ms
+        return wlo
 
     if wl in ("nvfp4", "nvfp4_w4a4"):
         from vflash_amd.nvfp4_linear import NVFP4Execution, NVFP4Weight
@@ -560,6 +590,10 @@ def main():
     }
     if w.extra is not None:
         line["unfused_reference_ms_per_step"] = w.extra()
+    if w.graph is not None:
+        graph = w.graph()
+        line["graph_ms_per_step"] = graph
+        line["graph_rate"] = rate(w.work, graph, w.unit)
     if device is not None:
         line["device_ms_per_step"] = device
         line["device_rate"] = rate(w.work, device, w.unit)

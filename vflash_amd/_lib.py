@@ -106,24 +106,45 @@ def call(name: str, *args) -> None:
     raise KernelError(f"{name}: {text}")
 
 
+# The per-call host path matters for launch-bound shapes (a skinny linear's
+# kernels take a few microseconds): device facts that cannot change during a
+# process are cached, and the stream comes from torch's raw accessor, which
+# returns the pointer without building a Stream object.
+
+
 @cache
-def _arch(index: int) -> str:
-    return torch.cuda.get_device_properties(index).gcnArchName
+def _cuda_present() -> bool:
+    return torch.cuda.is_available()
+
+
+@cache
+def _gfx950_index(index: int) -> bool:
+    return torch.cuda.get_device_properties(index).gcnArchName.split(":")[0] == "gfx950"
+
+
+def _index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
 
 
 def is_gfx950(device: torch.device) -> bool:
-    if device.type != "cuda" or not torch.cuda.is_available():
+    if device.type != "cuda" or not _cuda_present():
         return False
-    index = device.index if device.index is not None else torch.cuda.current_device()
-    return _arch(index).split(":")[0] == "gfx950"
+    return _gfx950_index(_index(device))
 
 
-def stream_of(device: torch.device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
-def ptr(tensor: torch.Tensor | None) -> ctypes.c_void_p | None:
-    return None if tensor is None else ctypes.c_void_p(tensor.data_ptr())
+def stream_of(device: torch.device) -> int:
+    """Address of the current HIP stream of ``device`` (what the C-ABI takes as ``stream``)."""
+    if _RAW_STREAM is not None:
+        return _RAW_STREAM(_index(device))
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(tensor: torch.Tensor | None) -> int | None:
+    """Device address of a tensor's first element, or None (NULL) for an absent operand."""
+    return None if tensor is None else tensor.data_ptr()
 
 
 def set_gemm_tile(tile: int, group_m: int = 0) -> int:

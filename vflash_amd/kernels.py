@@ -17,11 +17,11 @@ E4M3 = torch.float8_e4m3fn
 
 def require_device(*tensors: torch.Tensor) -> torch.device:
     device = tensors[0].device
-    if not _lib.is_gfx950(device):
-        raise ValueError("the HIP quantized-linear kernels require a gfx950 (MI355X) device")
-    for t in tensors:
+    for t in tensors[1:]:
         if t is not None and t.device != device:
             raise ValueError("all operands must share one device")
+    if not _lib.is_gfx950(device):
+        raise ValueError("the HIP quantized-linear kernels require a gfx950 (MI355X) device")
     return device
 
 
@@ -103,7 +103,7 @@ def _gemm_operands(codes, act_scale, weight, w_scale, rows, bias):
         bias.dtype != torch.bfloat16 or bias.shape != (weight.shape[0],) or not bias.is_contiguous()
     ):
         raise ValueError("GEMM bias must be a contiguous BF16 vector of the output width")
-    return require_device(codes, act_scale, weight, w_scale, *( [bias] if bias is not None else []))
+    return require_device(codes, act_scale, weight, w_scale, bias)
 
 
 def fp8_gemm(codes, act_scale, weight, w_scale, rows, bias=None, out=None):
@@ -297,7 +297,8 @@ def fp8_gemm_lora(codes, act_scale, weight, w_scale, rows, t, lora_b, *, scale=1
         raise ValueError("LoRA operands do not match the projection")
     if t.stride(1) != 1 or lora_b.stride(1) != 1:
         raise ValueError("LoRA operands need unit column stride")
-    require_device(t, lora_b)
+    if t.device != device or lora_b.device != device:
+        raise ValueError("all operands must share one device")
     out = torch.empty((rows, n), device=device, dtype=torch.bfloat16)
     if rows:
         call("vflash_fp8_linear_lora", ptr(codes), ptr(act_scale), codes.stride(0), ptr(weight),
