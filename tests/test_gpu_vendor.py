@@ -155,3 +155,57 @@ def test_ffn_matches_the_reference_composition(dev, activation, m, h, f):
           f"{codes_moved:.2e} (in {rows_moved:.3f} of the rows); max (|diff| - propagated) / "
           f"(addends + rms) {float((slack / (addends + rms)).max()):.3g}")
     assert exact > 0.9 and codes_moved < 1e-3
+
+
+def test_merged_qkv_planes_match_the_reference_call(dev):
+    # X [32760, 5120] against cat(Wq, Wk, Wv) [15360, 5120]: the reference makes
+    # one linear call and chunks it (h3_reference_execution.py:161-192); the
+    # planes here are written by the epilogue.
+    from vflash_amd.fused import merge_qkv, qkv_linear
+
+    m, hidden, inner = 32760, 5120, 5120
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn((m, hidden), generator=g).to(torch.bfloat16).to(dev)
+    parts = [quantize_weight_rows(torch.randn((inner, hidden), generator=g) * 0.02) for _ in range(3)]
+    b = (torch.randn(3 * inner, generator=g) * 0.01).to(torch.bfloat16).to(dev)
+    w, s = merge_qkv([p[0].to(dev) for p in parts], [p[1].to(dev) for p in parts])
+    ex = RowFP8Execution("w8a8", activation_quantizer="triton")
+    planes = qkv_linear(ex, x, w, s, b, planes=True)
+    a, sa = kernels.quantize_rows(x)
+    ref = reference_call(a, sa, w, s, b, m).chunk(3, dim=-1)
+    for name, got, want in zip("qkv", planes, ref):
+        o, r = got.float(), want.float()
+        rms = float(torch.sqrt(torch.mean(r * r)))
+        err = (o - r).abs()
+        assert int((err > 1e-2 * r.abs() + 1e-2 * rms).sum()) <= r.numel() // 10000
+        assert not bool((err > 2.0**-6 * r.abs() + 1e-2 * rms).any())
+        exact = float((o == r).float().mean())
+        print(f"[qkv {name} 32760x5120x5120] identical {exact:.5f}")
+        assert exact > 0.999
+
+
+@pytest.mark.parametrize("m", [256, 512, 1024])
+@pytest.mark.parametrize("n", [1536, 4608, 6144])
+def test_lora_linear_matches_the_reference_hook(dev, m, n):
+    # The adapter hook of h3_reference_lora.py:75-90 on the reference linear:
+    # delta = F.linear(F.linear(x, A), B) in bf16, * scaling, * strength (each
+    # rounded), result + delta.
+    from vflash_amd.fused import fp8_linear_lora
+
+    k, rank, scaling, strength = 1536, 32, 0.5, 1.375
+    x, codes, scale, b = inputs(m, k, n, seed=m * n)
+    g = torch.Generator().manual_seed(m + n + 1)
+    la = (torch.randn((rank, k), generator=g) * 0.01).to(torch.bfloat16).to(dev)
+    lb = (torch.randn((n, rank), generator=g) * 0.01).to(torch.bfloat16).to(dev)
+    xd, cd, sd, bd = x.to(dev), codes.to(dev), scale.to(dev), b.to(dev)
+    ex = RowFP8Execution("w8a8", activation_quantizer="hip")
+    ours = fp8_linear_lora(ex, xd, cd, sd, bd, la, lb, scaling=scaling, strength=strength)
+    a, sa = kernels.quantize_rows(xd)
+    result = reference_call(a, sa, cd, sd, bd, m)
+    delta = torch.nn.functional.linear(torch.nn.functional.linear(xd, la), lb).to(result.dtype)
+    delta = delta * scaling
+    delta = delta * strength
+    ref = result + delta
+    worst, exact = rel_check(ours.float().cpu().numpy(), ref.float().cpu().numpy())
+    print(f"[lora {m}x{k}x{n}] identical {exact:.5f}, worst relative difference {worst:.3g}")
+    assert exact > 0.999
