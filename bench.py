@@ -16,7 +16,10 @@ Other workloads (``qkv``, ``ffn``, ``ffn_swiglu``, ``skinny``, ``nvfp4`` (W4A8, 
 1 GiB device copy, the calibration kernel for the HBM byte counters.  For the
 launch-bound shapes (``small``, ``skinny``) the line adds a device-side time
 per step measured with the launch queue filled ahead; ``skinny`` also adds the
-step rate when each step is replayed from a captured HIP graph.
+step rate when each step is replayed from a captured HIP graph.  The
+``fp8_linear`` and ``small`` lines carry ``vendor_reference``: the reference's
+own GEMM call (``torch._scaled_mm`` with row-wise scales, hipBLASLt, + bias) on
+the same codes, timed the same way.
 """
 
 from __future__ import annotations
@@ -166,6 +169,8 @@ class Workload:
         self.extra = None  # optional comparison timing: () -> ms per step
         # Optional: () -> ms per step with the step replayed from captured HIP graphs.
         self.graph = None
+        # Optional: () -> dict, the reference's own library call timed on the same inputs.
+        self.vendor = None
 
 
 def rate(work, ms, unit):
@@ -225,8 +230,36 @@ def make_workload(args, dev):
         if wl == "qkv":
             config["output"] = "3 planes [32760, 40 heads, 128]"
         cpu = None if args.no_cpu_baseline else (lambda: cpu_baseline_weight_only(*host, 2.0 * n * k))
-        return Workload(wl, metric, "TFLOP/s", flops, step, "fp8_gemm", flops, "mfma",
-                        FP8_PEAK_TFLOPS, config, cpu=cpu, launch_bound=wl == "small")
+        wlo = Workload(wl, metric, "TFLOP/s", flops, step, "fp8_gemm", flops, "mfma",
+                       FP8_PEAK_TFLOPS, config, cpu=cpu, launch_bound=wl == "small")
+
+        def vendor():
+            # The reference's own GEMM call on the same codes and scales:
+            # torch._scaled_mm with row-wise scales (hipBLASLt on ROCm) + bias
+            # (h3_fp8_linear.py:109-121), timed like the GEMM above.
+            xd, cd, sd, bd = sets[0]
+            a, sa = kernels.quantize_rows(xd)
+
+            def call():
+                out = torch._scaled_mm(a, cd.t(), scale_a=sa, scale_b=sd.t(),
+                                       out_dtype=torch.bfloat16, use_fast_accum=False)
+                return out[:m] + bd
+
+            for _ in range(5):
+                call()
+            timer = EventTimer()
+            for _ in range(20):
+                timer.start()
+                call()
+                timer.stop()
+            torch.cuda.synchronize()
+            ms = statistics.mean(timer.times_ms())
+            return {"call": "torch._scaled_mm (row-wise scales, hipBLASLt) + bias", "ms": ms,
+                    "tflops": flops / (ms * 1e-3) / 1e12}
+
+        if wl != "qkv":
+            wlo.vendor = vendor
+        return wlo
 
     if wl in ("ffn", "ffn_swiglu"):
         from vflash_amd.fused import fp8_ffn
@@ -590,6 +623,8 @@ def main():
     }
     if w.extra is not None:
         line["unfused_reference_ms_per_step"] = w.extra()
+    if w.vendor is not None:
+        line["vendor_reference"] = w.vendor()
     if w.graph is not None:
         graph = w.graph()
         line["graph_ms_per_step"] = graph
