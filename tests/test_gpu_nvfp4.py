@@ -168,3 +168,43 @@ def test_hardware_e2m1_conversion_is_rne_on_every_clamped_binary32(dev):
     assert f[0] == "values" and int(f[1]) == 2 * (0x40C00000 + 1), result.stdout
     assert f[2] == "mismatches" and int(f[3]) == 0, result.stdout
     assert f[4] == "order_mismatches" and int(f[5]) == 0, result.stdout
+
+
+@pytest.mark.parametrize("activations", ["e4m3", "nvfp4"])
+def test_every_element_at_the_config_shape(dev, activations):
+    # X [32760, 5120], W e2m1 [13824, 5120]: every output element against an
+    # fp32 product of the exactly dequantized operands (the oracle's
+    # dequantization of the kernel's own activation codes; e2m1 x e4m3 and
+    # e4m3 x (e2m1 x e4m3) products are exact in binary32, so only the sum
+    # order differs from the kernel's).
+    m, n, k = 32760, 13824, 5120
+    x, (packed, scales, alpha, _), b = make(m, n, k, seed=23)
+    gsf = torch.tensor(2688.0 / float(x.float().abs().max()), dtype=torch.float32)
+    weight = NVFP4Weight(packed.to(dev), scales.to(dev), alpha.to(dev), gsf.to(dev))
+    xd = x.to(dev)
+    out = NVFP4Execution(activations).linear(xd, weight, b.to(dev))
+    w_dq = torch.from_numpy(N.dequantize_weight(packed.numpy(), scales.numpy()).astype(np.float32)).to(dev)
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        if activations == "e4m3":
+            codes, sa = kernels.quantize_rows(xd)
+            acc = torch.matmul(codes[:m].float(), w_dq.t().contiguous())
+            y = acc * sa[:m] * float(alpha)
+        else:
+            codes, a_scales = kernels.nvfp4_quantize_rows(xd, gsf.to(dev))
+            a_dq = torch.from_numpy(
+                N.dequantize_weight(codes.cpu().numpy(), a_scales.cpu().numpy()).astype(np.float32)).to(dev)
+            out_scale = np.float32(float(alpha)) / np.float32(float(gsf))  # one fp32 division, as on the device
+            y = torch.matmul(a_dq, w_dq.t().contiguous()) * float(out_scale)
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = prev
+    ref = (y.to(torch.bfloat16) + b.to(dev)).float()
+    o = out.float()
+    rms = float(torch.sqrt(torch.mean(ref * ref)))
+    err = (o - ref).abs()
+    assert int((err > 1e-2 * ref.abs() + 1e-2 * rms).sum()) <= ref.numel() // 10000
+    assert not bool((err > 2.0**-6 * ref.abs() + 1e-2 * rms).any())
+    exact = float((o == ref).float().mean())
+    print(f"[nvfp4 {activations} {m}x{k}x{n}] identical {exact:.6f}")
+    assert exact > 0.9999
