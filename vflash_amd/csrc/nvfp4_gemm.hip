@@ -357,14 +357,23 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
 
   v16f acc[NB][MB];
   static_for<NB>([&](auto i) { static_for<MB>([&](auto jj) { acc[i][jj] = v16f{}; }); });
+  // Block scales of the current 16-K block as binary16 pairs: steps 2b and
+  // 2b + 1 of a half share block b, so each is converted once per two steps.
+  v2h scw[NB], sca[A4 ? MB : 1];
   // MFMA step v (0..3) of a half held in r.
   auto step = [&](const Raw& r, auto v) {
     v8h xa[MB], xw[NB];
-    // Eight E2M1 values of packed word d times their E4M3 block scale (byte
-    // 2*fh + v/2 of the row's scale word), exact in binary16.
-    auto fp4x8 = [&](uint32_t d, uint32_t sword) {
+    // E4M3 block scale (byte 2*fh + v/2 of the row's scale word), exact in binary16.
+    auto scale_pair = [&](uint32_t sword) {
       const uint32_t sb = (sword >> (16 * fh + 8 * (v / 2))) & 0xffu;
-      const v2h sc = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(sb | (sb << 8), 1.0f, false);
+      return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(sb | (sb << 8), 1.0f, false);
+    };
+    if constexpr (v % 2 == 0) {
+      static_for<NB>([&](auto nb) { scw[nb] = scale_pair(r.s[nb]); });
+      if constexpr (A4) static_for<MB>([&](auto mb) { sca[mb] = scale_pair(r.as[mb]); });
+    }
+    // Eight E2M1 values of packed word d times their block scale sc, exact in binary16.
+    auto fp4x8 = [&](uint32_t d, v2h sc) {
       const v2h y0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.0f, 0) * sc;
       const v2h y1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.0f, 1) * sc;
       const v2h y2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.0f, 2) * sc;
@@ -373,7 +382,7 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
     };
     static_for<MB>([&](auto mb) {
       if constexpr (A4) {
-        xa[mb] = fp4x8((uint32_t)r.a[mb][0][(int)v], r.as[mb]);
+        xa[mb] = fp4x8((uint32_t)r.a[mb][0][(int)v], sca[mb]);
       } else {
         const uint32_t d0 = (uint32_t)r.a[mb][v / 2][(v % 2) * 2];
         const uint32_t d1 = (uint32_t)r.a[mb][v / 2][(v % 2) * 2 + 1];
@@ -384,7 +393,7 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
         xa[mb] = v8h{x0[0], x0[1], x1[0], x1[1], x2[0], x2[1], x3[0], x3[1]};
       }
     });
-    static_for<NB>([&](auto nb) { xw[nb] = fp4x8((uint32_t)r.w[nb][(int)v], r.s[nb]); });
+    static_for<NB>([&](auto nb) { xw[nb] = fp4x8((uint32_t)r.w[nb][(int)v], scw[nb]); });
     static_for<NB>([&](auto nb) {
       static_for<MB>([&](auto mb) {
         acc[nb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xw[nb], xa[mb], acc[nb][mb], 0, 0, 0);
