@@ -188,3 +188,16 @@ def test_nvfp4_unsupported_device_refuses_and_counts_nothing():
     with pytest.raises(ValueError, match="inference-only"):
         ex.linear(torch.ones((1, 64), requires_grad=True), nv_weight())
     assert ex.calls == 0 and ex.rows == 0
+
+
+def test_bench_measures_one_gpu_only():
+    # This path is measured on one MI355X; several GPUs are a design note.
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    result = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"],
+                            capture_output=True, text=True, timeout=120)
+    assert result.returncode != 0
+    assert "one GPU" in result.stderr + result.stdout
