@@ -68,6 +68,13 @@ def rmsnorm_modulate_quantize(matrix, norm_weight, scale, shift, *, eps, index=N
         norm_weight.dtype != torch.bfloat16 or norm_weight.shape != (k,) or not norm_weight.is_contiguous()
     ):
         raise ValueError("the RMSNorm weight must be a contiguous BF16 [K] vector")
+    if m == 0:
+        # No tokens (an empty sequence gathers no modulation rows): empty outputs.
+        device = require_device(matrix, scale, shift, norm_weight, index)
+        codes = torch.empty((0, k), device=device, dtype=E4M3)
+        scales = torch.empty((0, 1), device=device, dtype=torch.float32)
+        values = torch.empty((0, k), device=device, dtype=torch.bfloat16) if keep_values else None
+        return codes, scales, values
     if index is not None:
         if index.dtype != torch.int64 or index.ndim != 1 or not index.is_contiguous() or index.numel() < 1:
             raise ValueError("modulation indices must be a contiguous int64 vector")
