@@ -719,11 +719,22 @@ static hipError_t launch_cfg(const GemmParams& p, hipStream_t s) {
 // 11 = tile 10 as a persistent kernel (one workgroup per CU),
 // 12 = 128x128 two-slot pipelined (2x2 waves of 64x64, two workgroups per CU),
 // 13 / 14 = 128x128 with four / three stage slots (one workgroup per CU).
+//
+// Automatic choice: the 64x64 tile below 256 tiles of 128x128, else whichever of
+// tile 17 (256x256, one workgroup per CU) and tile 12 (128x128, two per CU)
+// needs fewer rounds of tiles, a 128x128 round counting 0.5 x 1.15 of a 256x256
+// round (a quarter of the work at two per CU, at the 128x128 tile's lower
+// efficiency).  The model gives the measured ratios: 1.16 in favour of tile 17 at
+// 4096x3072x3072 (192 against 768 tiles) and 1.74 in favour of tile 12 at
+// M=1024, K=1536, N=6144 (96 against 384 tiles).
+int compute_units();
 int pick_tile(const GemmParams& p) {
   auto tiles = [&](int bm, int bn) { return ((p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn); };
-  if (tiles(256, 256) >= 512) return 17;
-  if (tiles(128, 128) >= 256) return 12;
-  return 3;
+  const int64_t t128 = tiles(128, 128), t256 = tiles(256, 256), cus = compute_units();
+  if (t128 < 256) return 3;
+  const double rounds256 = (double)((t256 + cus - 1) / cus);
+  const double rounds128 = (double)((t128 + 2 * cus - 1) / (2 * cus)) * 0.5 * 1.15;
+  return rounds256 <= rounds128 ? 17 : 12;
 }
 
 template <int EPI>
