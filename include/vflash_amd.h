@@ -289,7 +289,10 @@ int vflash_nvfp4_w4a4_linear(const void* a, int64_t lda, const void* a_scales, c
  * tile 17's schedule, 19 = tile 17 as a persistent grid whose epilogue stores
  * from registers while the next tile's first stages load)
  * and the tile-order group height (0 = default: 2 for the E4M3 GEMMs, 8 for the
- * E2M1-weight ones).  For vflash_nvfp4_linear the
+ * E2M1-weight ones).  The automatic E4M3 choice is 3 below 256 tiles of
+ * 128x128, else 17 or 12, whichever needs fewer rounds of tiles over the
+ * compute units (a 128x128 round, two workgroups per CU, weighted 0.575 of a
+ * 256x256 round).  For vflash_nvfp4_linear the
  * values mean 1 = 256x256, 2 = 128x128, 3 = 64x128 (register-staged) and
  * 4 = 256x256 pipelined (default for large shapes); other values select the
  * automatic choice there.  Returns the previous tile value.
