@@ -279,15 +279,14 @@ int vflash_nvfp4_w4a4_linear(const void* a, int64_t lda, const void* a_scales, c
  * Tuning hook: force a GEMM tile configuration for later calls in this process
  * (0 = automatic, 1 = 256x256, 2 = 128x128, 3 = 64x64, 4 = 128x256, 5 = 256x128,
  * 6 = 256x256 with 8 waves 4x2, 7 = 256x256 with 8 waves 2x4,
- * 8 / 9 = 256x256 five-stage LDS-DMA ring with 4 / 8 waves,
  * 10 = 256x256 two-slot 128-byte-stage LDS-DMA pipeline,
- * 11 = tile 10 as a persistent grid of one workgroup per CU,
  * 12 = 128x128 two-slot pipeline, two workgroups per CU,
  * 13 / 14 = 128x128 with four / three stage slots,
  * 15 = tile 10 with the stage barrier after K-substep 0, 16 = tile 10 with
  * scalar-offset DMA, 17 = both (default for large shapes), 18 = tile 12 with
  * tile 17's schedule, 19 = tile 17 as a persistent grid whose epilogue stores
- * from registers while the next tile's first stages load)
+ * from registers while the next tile's first stages load; other values,
+ * including 8, 9 and 11, leave the current configuration unchanged)
  * and the tile-order group height (0 = default: 2 for the E4M3 GEMMs, 8 for the
  * E2M1-weight ones).  The automatic E4M3 choice is 3 below 256 tiles of
  * 128x128, else 17 or 12, whichever needs fewer rounds of tiles over the

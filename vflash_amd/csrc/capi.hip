@@ -99,7 +99,7 @@ const char* vflash_status_string(int s) {
 
 int vflash_set_gemm_tile(int tile, int group_m) {
   const int prev = g_tile;
-  if (tile >= 0 && tile <= 19) g_tile = tile;
+  if (tile >= 0 && tile <= 19 && tile != 8 && tile != 9 && tile != 11) g_tile = tile;
   g_group_m = group_m > 0 ? group_m : 0;
   return prev;
 }

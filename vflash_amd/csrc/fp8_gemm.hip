@@ -149,137 +149,6 @@ __global__ void __launch_bounds__(64 * WGM * WGN) fp8_gemm_kernel(const GemmPara
 }
 
 // ---------------------------------------------------------------------------
-// Pipelined 256x256 main loop.
-//
-// K advances 64 bytes per stage.  A ring of NS = 5 LDS stages (32 KB each:
-// A and W halves of 256 rows x 64 bytes) is filled by buffer-load-to-LDS DMA
-// (buffer_load_dwordx4 ... lds), issued NS - 1 stages ahead of the stage being
-// multiplied, so global latency is covered by three stages of MFMA work and no
-// VGPRs are spent on staging.  The DMA is issued as inline assembly, so the
-// waits below are the only ones that order it against the fragment reads.
-// Per stage:
-//   wait for this wave's DMA of stage kt+1 and its own LDS reads, s_barrier;
-//   issue the DMA of stage kt+NS into the slot just consumed;
-//   run the MFMAs of stage kt from registers while reading the fragments of
-//   stage kt+1 from LDS into the other register set.
-// LDS rows are 64 bytes (four 16-byte chunks); chunk c of row r sits in slot
-// c ^ ((r >> 2) & 3), which keeps the 16 rows of one ds_read_b128 pass on
-// distinct bank groups of the 256-byte-wide LDS.
-template <int WGM, int WGN, int EPI>
-__global__ void __launch_bounds__(64 * WGM * WGN) fp8_gemm_pipe(const GemmParams p) {
-  constexpr int BM = 256, BN = 256, BK = 64, NS = 5;
-  constexpr int UN = NS % 2 ? 2 * NS : NS;  // unroll: ring slot and fragment set both static
-  constexpr int NW = WGM * WGN;
-  constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
-  constexpr int HALF = BM * BK;                // bytes of one operand per stage
-  constexpr int DMA_A = HALF / 1024 / NW;      // 1 KB DMA instructions per wave
-  constexpr int DMA = 2 * DMA_A;               // per wave per stage (A and W)
-  static_assert(DMA_A >= 1 && NS >= 3, "ring shape");
-  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * 2 * HALF];
-  static_assert(NS * 2 * HALF >= BM * BN * 2, "the ring doubles as the epilogue staging tile");
-  auto slot = [&](auto j) -> uint8_t* { return ring + j * 2 * HALF; };
-  const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(ring));
-
-  const int tiles_m = (int)((p.m + BM - 1) / BM);
-  const int tiles_n = (int)((p.n + BN - 1) / BN);
-  int tm, tn;
-  tile_coords(tiles_m, tiles_n, p.group_m, tm, tn);
-  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave % WGM, wn = wave / WGM;
-
-  const int64_t rows_a = min((int64_t)BM, p.m - m0);
-  const int64_t rows_w = min((int64_t)BN, p.n - n0);
-  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + m0 * p.lda, (uint32_t)(rows_a * p.lda));
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w + n0 * p.ldw, (uint32_t)(rows_w * p.ldw));
-
-  // DMA lane map: block b (1 KB) of an operand holds rows 16b..16b+15; lane l
-  // fills row 16b + l/4, slot l%4, from logical chunk (l%4) ^ swizzle(row).
-  const int drow = lane >> 2;
-  const int dchunk = (lane & 3) ^ ((drow >> 2) & 3);
-  uint32_t a_off[DMA_A], w_off[DMA_A];
-  static_for<DMA_A>([&](auto j) {
-    const int row = (wave * DMA_A + j) * 16 + drow;
-    a_off[j] = (uint32_t)(row * p.lda + dchunk * 16);
-    w_off[j] = (uint32_t)(row * p.ldw + dchunk * 16);
-  });
-  const int KT = (int)((p.k + BK - 1) / BK);
-
-  // DMA of stage s into ring slot j; chunks at or past K (including whole
-  // stages past the end) are pointed beyond the buffer and arrive as zeros.
-  const uint32_t wave_lds = ring_lds + __builtin_amdgcn_readfirstlane(wave) * DMA_A * 1024;
-  auto issue = [&](auto j, int s) {
-    const uint32_t base = wave_lds + j * 2 * HALF;
-    const int64_t kk = (int64_t)s * BK + dchunk * 16;
-    const uint32_t kill = kk < p.k ? 0u : VFA_OOB;
-    const uint32_t kb = (uint32_t)s * BK;
-    static_for<DMA_A>([&](auto i) { lds_dma16(ra, base + i * 1024, (a_off[i] + kb) | kill); });
-    static_for<DMA_A>([&](auto i) {
-      lds_dma16(rw, base + HALF + i * 1024, (w_off[i] + kb) | kill);
-    });
-  };
-
-  const int fr = lane & 31, fh = lane >> 5;
-  const int fsw = (fr >> 2) & 3;
-  const int o0 = ((fh * 2) ^ fsw) << 4, o1 = ((fh * 2 + 1) ^ fsw) << 4;
-  v8i F[2][MB + NB];  // fragment sets: [0, MB) activation blocks, [MB, MB+NB) weight blocks
-  auto read = [&](auto j, auto fb) {
-    const uint8_t* sa = slot(j) + (wm * WM + fr) * BK;
-    const uint8_t* sw = slot(j) + HALF + (wn * WN + fr) * BK;
-    static_for<MB + NB>([&](auto f) {
-      const uint8_t* src = f < MB ? sa + f * 32 * BK : sw + (f - MB) * 32 * BK;
-      const v4i lo = *reinterpret_cast<const v4i*>(src + o0);
-      const v4i hi = *reinterpret_cast<const v4i*>(src + o1);
-      F[fb][f] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    });
-  };
-
-  v16f acc[NB][MB];
-  static_for<NB>([&](auto i) { static_for<MB>([&](auto jj) { acc[i][jj] = v16f{}; }); });
-
-  // Wait until at most n of this wave's newest DMAs are in flight and its own
-  // LDS reads are done, then meet the other waves.
-  auto wait_stage = [&](auto inflight) {
-    wait_vmcnt<decltype(inflight)::value, true>();
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-  };
-
-  static_for<NS>([&](auto j) { issue(j, (int)j); });
-  wait_stage(std::integral_constant<int, DMA * (NS - 1)>{});
-  read(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
-
-  for (int kt0 = 0; kt0 < KT; kt0 += UN) {
-    static_for<UN>([&](auto u) {
-      const int kt = kt0 + u;
-      if (kt < KT) {
-        constexpr int j = u % NS, fb = u % 2;
-        wait_stage(std::integral_constant<int, DMA * (NS - 2)>{});
-        issue(std::integral_constant<int, j>{}, kt + NS);
-        static_for<NB>([&](auto nb) {
-          static_for<MB>([&](auto mb) {
-            acc[nb][mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                F[fb][MB + nb], F[fb][mb], acc[nb][mb], 0, 0, 0, 0, 0, 0);
-          });
-        });
-        // Fragments of stage kt+1 (slot contents are unused after the last stage).
-        read(std::integral_constant<int, (j + 1) % NS>{}, std::integral_constant<int, 1 - fb>{});
-        // One fragment read after each MFMA while the MFMA pipe is busy.
-        static_for<(MB * NB < 2 * (MB + NB) ? MB * NB : 2 * (MB + NB))>([&](auto) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        });
-      }
-    });
-  }
-  wait_vmcnt<0, true>();  // every ring DMA has landed before the ring is reused
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-  gemm_epilogue<BM, BN, WGM, WGN, EPI>(p, acc, m0, n0, wm, wn, (int)threadIdx.x, ring);
-}
-
-// ---------------------------------------------------------------------------
 // Two-slot pipelined 256x256 main loop with 128-byte K stages.
 //
 // Each stage holds 128 bytes of K for all 256 A rows and 256 W rows (64 KB);
@@ -582,47 +451,11 @@ __global__ void __launch_bounds__(256, NS == 2 ? 2 : 1) fp8_gemm_pipe2s(const Ge
                            __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6));
 }
 
-// Persistent form: one workgroup per CU walks its share of the tiles, so the
-// epilogue stores of one tile drain while the next tile's first stages load.
-// Workgroup b runs on XCD b % 8; XCD x owns the x-th contiguous run of logical
-// tiles (grouped order), handed round-robin to the XCD's workgroups.
-template <int EPI>
-__global__ void __launch_bounds__(256) fp8_gemm_persist(const GemmParams p) {
-  __shared__ __attribute__((aligned(1024))) uint8_t ring[PIPE2_LDS];
-  __shared__ __attribute__((aligned(1024))) uint8_t vec[VEC_LDS];
-  const int tiles_m = (int)((p.m + 255) / 256), tiles_n = (int)((p.n + 255) / 256);
-  const int T = tiles_m * tiles_n, G = gridDim.x, b = blockIdx.x;
-  int first, end, stride;
-  if (G >= 8 && (G & 7) == 0) {
-    const int x = b & 7, q = T >> 3, rem = T & 7;
-    first = x * q + min(x, rem) + (b >> 3);
-    end = x * q + min(x, rem) + q + (x < rem ? 1 : 0);
-    stride = G >> 3;
-  } else {
-    first = b;
-    end = T;
-    stride = G;
-  }
-  // Scalars materialized once: the work-item id is dead afterwards.
-  int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-  uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(ring));
-  uint32_t vec_lds = __builtin_amdgcn_readfirstlane(lds_addr(vec));
-  asm volatile("" : "+s"(wave), "+s"(ring_lds), "+s"(vec_lds));
-  for (int logical = first; logical < end; logical += stride) {
-    int tm, tn;
-    grouped_tile(logical, tiles_m, tiles_n, p.group_m, tm, tn);
-    pipe2_tile<EPI>(p, tm, tn, ring, ring_lds, vec, vec_lds, wave);
-    // Every wave has read its staged rows before the next tile's DMA reuses them.
-    wait_vmcnt<63, true>();
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-  }
-}
-
-// Persistent 256x256 EPI_BIAS form with the direct-store epilogue: tile i's
-// stores drain while tile i+1's first stages load (tiles as fp8_gemm_persist
-// assigns them).
+// Persistent 256x256 EPI_BIAS form with the direct-store epilogue: one
+// workgroup per CU walks its share of the tiles, and tile i's stores drain
+// while tile i+1's first stages load.  Workgroup b runs on XCD b % 8; XCD x
+// owns the x-th contiguous run of logical tiles (grouped order), handed
+// round-robin to the XCD's workgroups.
 template <int PRE>
 __global__ void __launch_bounds__(256) fp8_gemm_persist2(const GemmParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t ring[PIPE2_LDS];
@@ -688,20 +521,7 @@ static hipError_t launch_pipe2s(const GemmParams& p, hipStream_t s) {
 
 int compute_units();
 
-template <int EPI>
-static hipError_t launch_persist(const GemmParams& p, hipStream_t s) {
-  const int64_t tiles = ((p.m + 255) / 256) * ((p.n + 255) / 256);
-  const int64_t grid = tiles < compute_units() ? tiles : compute_units();
-  fp8_gemm_persist<EPI><<<dim3((unsigned)grid), dim3(256), 0, s>>>(p);
-  return hipGetLastError();
-}
 
-template <int WGM, int WGN, int EPI>
-static hipError_t launch_pipe(const GemmParams& p, hipStream_t s) {
-  const int64_t tiles = ((p.m + 255) / 256) * ((p.n + 255) / 256);
-  fp8_gemm_pipe<WGM, WGN, EPI><<<dim3((unsigned)tiles), dim3(64 * WGM * WGN), 0, s>>>(p);
-  return hipGetLastError();
-}
 
 template <int BM, int BN, int WGM, int WGN, int EPI>
 static hipError_t launch_cfg(const GemmParams& p, hipStream_t s) {
@@ -714,10 +534,9 @@ static hipError_t launch_cfg(const GemmParams& p, hipStream_t s) {
 // 1 = 256x256 (2x2), 2 = 128x128 (2x2), 3 = 64x64 (2x2; 128x128 for GELU,
 // whose row maxima need 64-column wave groups), 4 = 128x256 (2x2),
 // 5 = 256x128 (2x2), 6 = 256x256 (4x2: two waves per SIMD),
-// 7 = 256x256 (2x4: two waves per SIMD), 8 = 256x256 pipelined (2x2),
-// 9 = 256x256 pipelined (2x4), 10 = 256x256 two-slot pipelined, 128-byte stages,
-// 11 = tile 10 as a persistent kernel (one workgroup per CU),
-// 12 = 128x128 two-slot pipelined (2x2 waves of 64x64, two workgroups per CU),
+// 7 = 256x256 (2x4: two waves per SIMD), 10 = 256x256 two-slot pipelined,
+// 128-byte stages, 12 = 128x128 two-slot pipelined (2x2 waves of 64x64, two
+// workgroups per CU),
 // 13 / 14 = 128x128 with four / three stage slots (one workgroup per CU).
 //
 // Automatic choice: the 64x64 tile below 256 tiles of 128x128, else whichever of
@@ -749,10 +568,7 @@ hipError_t launch_epi(const GemmParams& p, int tile, hipStream_t s) {
     case 5: return launch_cfg<256, 128, 2, 2, EPI>(p, s);
     case 6: return launch_cfg<256, 256, 4, 2, EPI>(p, s);
     case 7: return launch_cfg<256, 256, 2, 4, EPI>(p, s);
-    case 8: return launch_pipe<2, 2, EPI>(p, s);
-    case 9: return launch_pipe<2, 4, EPI>(p, s);
     case 10: return launch_pipe2<EPI>(p, s);
-    case 11: return launch_persist<EPI>(p, s);
     case 12: return launch_pipe2s<EPI, 2>(p, s);
     case 13: return launch_pipe2s<EPI, 4>(p, s);
     case 14: return launch_pipe2s<EPI, 3>(p, s);
