@@ -93,3 +93,16 @@ def test_gate_residual_and_producer_contracts():
     args[5] = 1e-6
     args[7] = 20
     assert lib.vflash_rmsnorm_modulate_quantize_e4m3(*args) == -1
+
+
+def test_tuning_hook_keeps_only_existing_configurations():
+    lib = _lib.library()
+    prev = lib.vflash_set_gemm_tile(17, 0)
+    try:
+        # 8, 9, 11 and out-of-range values are not configurations: unchanged.
+        for bad in (8, 9, 11, 20, -1):
+            assert lib.vflash_set_gemm_tile(bad, 0) == 17
+        assert lib.vflash_set_gemm_tile(12, 0) == 17
+        assert lib.vflash_set_gemm_tile(0, 0) == 12
+    finally:
+        lib.vflash_set_gemm_tile(prev, 0)
