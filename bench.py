@@ -629,9 +629,12 @@ def main():
         except (RuntimeError, NotImplementedError) as err:  # a torch without row-wise FP8 GEMMs
             line["vendor_reference"] = {"error": str(err).splitlines()[0][:200]}
     if w.graph is not None:
-        graph = w.graph()
-        line["graph_ms_per_step"] = graph
-        line["graph_rate"] = rate(w.work, graph, w.unit)
+        try:
+            graph = w.graph()
+            line["graph_ms_per_step"] = graph
+            line["graph_rate"] = rate(w.work, graph, w.unit)
+        except RuntimeError as err:  # a runtime that cannot capture the step
+            line["graph_ms_per_step"] = {"error": str(err).splitlines()[0][:200]}
     if device is not None:
         line["device_ms_per_step"] = device
         line["device_rate"] = rate(w.work, device, w.unit)
