@@ -9,7 +9,9 @@ with the scale/bias epilogue.  Inputs are seeded synthetic tensors already in
 HBM.  A step is one ``linear`` call; K timed steps are bracketed by
 ``torch.cuda.synchronize()``.  The dominant kernel (the GEMM) is timed with HIP
 events recorded on the launch stream around each of its launches in the timed
-region.  Prints one JSON line.
+region, placed by the execution's ``measure`` scope hook (the reference's
+profiling interface), so the timed step is the drop-in call itself.  Prints one
+JSON line.
 
 Other workloads (``qkv``, ``ffn``, ``ffn_swiglu``, ``skinny``, ``nvfp4`` (W4A8, as configured),
 ``nvfp4_w4a4``, ``small``, ``norm_quant``) print the same kind of line for the other shapes of this path; ``copy`` times a plain
@@ -54,8 +56,6 @@ def parse():
     p.add_argument("--operand-sets", type=int, default=0,
                    help="rotating operand sets for the small shapes (0 = enough to exceed the last-level cache)")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--tile", type=int, default=0, help="force a GEMM tile configuration")
-    p.add_argument("--group-m", type=int, default=0)
     return p.parse_args()
 
 
@@ -85,13 +85,68 @@ def traffic_from_profiles(workload: str):
     return None
 
 
-def cpu_baseline_weight_only(x, codes, scale, b, flops_per_row):
-    """The reference's CPU weight-only path on a bounded row sample."""
+def host_threads() -> int:
+    """Threads for the CPU baselines: every core this process may run on
+    (os.cpu_count() narrowed by the CPU affinity), capped by OMP_NUM_THREADS
+    when the host sets it (a GPU box's share of the host)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def use_host_threads() -> int:
     import torch
 
+    threads = host_threads()
+    torch.set_num_threads(threads)
+    return threads
+
+
+def cpu_oracle_linear(x, codes, scale, b, flops_per_row):
+    """The CPU W8A8 emulation oracle (per-token E4M3 quantization, exact binary64
+    sums, bf16(acc * sa * sw), bf16(+ bias)) timed on a row sample: the parity
+    reference, reported beside the baseline but not the baseline."""
+    from oracle import fp8 as O
+
+    threads = use_host_threads()
+    wc = codes.view(__import__("torch").uint8).numpy()
+    sw = scale.reshape(-1).numpy()
+    bias = None if b is None else b.float().numpy()
+    rows = 16
+    O.w8a8_linear(x[:rows].float().numpy(), wc, sw, bias)  # warm-up
+    t0 = time.perf_counter()
+    O.w8a8_linear(x[:rows].float().numpy(), wc, sw, bias)
+    probe = time.perf_counter() - t0
+    rows = int(min(x.shape[0], max(16, 16 * 3.0 / max(probe, 1e-3))) // 16 * 16)
+    t0 = time.perf_counter()
+    O.w8a8_linear(x[:rows].float().numpy(), wc, sw, bias)
+    dt = time.perf_counter() - t0
+    return {"value": flops_per_row * rows / dt / 1e12, "unit": "TFLOP/s", "threads": threads,
+            "cpu_model": cpu_model(),
+            "sample": (f"numpy W8A8 oracle (binary64 sums of decoded E4M3 products) on {rows} of "
+                       f"{x.shape[0]} rows, {dt * 1e3:.0f} ms")}
+
+
+def cpu_baseline_weight_only(x, codes, scale, b, flops_per_row):
+    """The reference's CPU weight-only path on a bounded row sample."""
     from oracle.baseline import weight_only_linear
 
-    threads = torch.get_num_threads()
+    threads = use_host_threads()
     rows = 128
     t0 = time.perf_counter()
     weight_only_linear(x[:rows], codes, scale, b)
@@ -109,6 +164,8 @@ def cpu_baseline_weight_only(x, codes, scale, b, flops_per_row):
         "value": flops_per_row * rows / t / 1e12,
         "unit": "TFLOP/s",
         "cores": threads,
+        "threads": threads,
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": (
             f"weight-only dequant-matmul (restored bf16 W every call, F.linear + bias; "
@@ -146,6 +203,34 @@ class EventTimer:
         return [s.elapsed_time(e) for s, e in self.pairs]
 
 
+class ScopeTimer:
+    """``measure`` hook of a RowFP8Execution that brackets the first
+    ``linear.fp8_gemm`` scope of each armed step with the timer's events (the
+    dominant GEMM launch of the drop-in call: the linear's GEMM, the FFN's up
+    projection); every other scope is a no-op."""
+
+    def __init__(self):
+        self.timer = None
+
+    def arm(self, timer):
+        self.timer = timer
+
+    def __call__(self, name):
+        from contextlib import contextmanager, nullcontext
+
+        if name != "linear.fp8_gemm" or self.timer is None:
+            return nullcontext()
+        timer, self.timer = self.timer, None
+
+        @contextmanager
+        def scope():
+            timer.start()
+            yield
+            timer.stop()
+
+        return scope()
+
+
 class Workload:
     """One shape of the path: its step, the dominant kernel and its roofline units."""
 
@@ -171,6 +256,10 @@ class Workload:
         self.graph = None
         # Optional: () -> dict, the reference's own library call timed on the same inputs.
         self.vendor = None
+        # Optional: () -> dict, the CPU W8A8 emulation oracle timed on a row sample.
+        self.cpu_oracle = None
+        # Also report the kernel's fraction of the FP8 MFMA peak (16-bit MFMA kernels).
+        self.fp8_frac = False
 
 
 def rate(work, ms, unit):
@@ -203,22 +292,19 @@ def make_workload(args, dev):
         m, k, n = {"fp8_linear": (32760, 5120, 13824), "small": (4096, 3072, 3072),
                    "qkv": (32760, 5120, 15360)}[wl]
         host, sets = linear_sets(m, k, n, (args.operand_sets or 8) if wl == "small" else 1, dev)
-        ex = RowFP8Execution("w8a8", activation_quantizer="hip")
-        # One call through the module API checks the drop-in path end to end; the
-        # timed step is the same pair of launches that RowFP8Execution.linear makes.
-        ex.linear(sets[0][0][:16], *sets[0][1:])
+        scope = ScopeTimer()
+        ex = RowFP8Execution("w8a8", activation_quantizer="hip", measure=scope)
+        from vflash_amd.fused import qkv_linear
 
         def step(i, timer):
+            # The drop-in call: RowFP8Execution.linear, or the merged QKV linear
+            # writing three planes.
             xd, cd, sd, bd = sets[i % len(sets)]
-            a, sa = kernels.quantize_rows(xd)
-            if timer:
-                timer.start()
+            scope.arm(timer)
             if wl == "qkv":
-                kernels.fp8_gemm_planes(a, sa, cd, sd, m, 3, bd)
+                qkv_linear(ex, xd, cd, sd, bd, planes=True)
             else:
-                kernels.fp8_gemm(a, sa, cd, sd, m, bd)
-            if timer:
-                timer.stop()
+                ex.linear(xd, cd, sd, bd)
 
         flops = 2.0 * m * n * k
         names = {"fp8_linear": "fp8_linear_m32760_k5120_n13824", "small": "fp8_linear_m4096_k3072_n3072",
@@ -259,6 +345,8 @@ def make_workload(args, dev):
 
         if wl != "qkv":
             wlo.vendor = vendor
+        if not args.no_cpu_baseline and wl != "qkv":
+            wlo.cpu_oracle = lambda: cpu_oracle_linear(*host, 2.0 * n * k)
         return wlo
 
     if wl in ("ffn", "ffn_swiglu"):
@@ -280,33 +368,28 @@ def make_workload(args, dev):
         cu, su = quantize_weight_rows(wu)
         cdn, sdn = quantize_weight_rows(wdn)
         t = [v.to(dev) for v in (x, cu, su, bu, cdn, sdn, bdn, gate, res)]
-        ex = RowFP8Execution("w8a8", activation_quantizer="hip")
+        scope = ScopeTimer()
+        ex = RowFP8Execution("w8a8", activation_quantizer="hip", measure=scope)
         act = "swiglu" if swiglu else "gelu_tanh"
-        fp8_ffn(ex, t[0][:64], t[1], t[2], t[3], t[4], t[5], t[6], t[7], t[8][:64], activation=act)
-        up_kernel = kernels.fp8_gemm_swiglu if swiglu else kernels.fp8_gemm_gelu
 
         def step(i, timer):
-            a, sa = kernels.quantize_rows(t[0])
-            if timer:
-                timer.start()
-            gg, amax = up_kernel(a, sa, t[1], t[2], m, t[3])
-            if timer:
-                timer.stop()
-            hc, hs = kernels.requant_rows(gg, amax)
-            kernels.fp8_gemm_gate_residual(hc, hs, t[4], t[5], m, t[7], t[8], t[6])
+            # The drop-in call; the scope hook times its first GEMM (the up projection).
+            scope.arm(timer)
+            fp8_ffn(ex, t[0], t[1], t[2], t[3], t[4], t[5], t[6], t[7], t[8], activation=act)
 
         cpu = None
         if not args.no_cpu_baseline and not swiglu:
             from oracle.baseline import gelu_ffn
 
             def cpu():
+                threads = use_host_threads()
                 rows = 256
                 gelu_ffn(x[:32], cu, su, bu, cdn, sdn, bdn, gate, res[:32])  # warm-up
                 t0 = time.perf_counter()
                 gelu_ffn(x[:rows], cu, su, bu, cdn, sdn, bdn, gate, res[:rows])
                 dt = time.perf_counter() - t0
                 return {"value": 4.0 * h * f * rows / dt / 1e12, "unit": "TFLOP/s",
-                        "cores": torch.get_num_threads(), "kind": "port",
+                        "cores": threads, "threads": threads, "cpu_model": cpu_model(), "kind": "port",
                         "sample": (f"weight-only FFN chain (dequantized bf16 weights, GELU-tanh, "
                                    f"gate-residual) on {rows} of {m} rows, one call after a warm-up")}
 
@@ -319,9 +402,9 @@ def make_workload(args, dev):
                  "step": "quant, packed up GEMM + SwiGLU + row amax, requant, down GEMM + gate-residual"})
         return Workload(
             wl, "Fused FP8 FFN TFLOP/s (M=32760, 5120 -> 13824 GELU-tanh -> 5120, gate-residual)",
-            "TFLOP/s", 4.0 * m * h * f, step, "fp8_gemm_gelu", 2.0 * m * h * f, "mfma", FP8_PEAK_TFLOPS,
+            "TFLOP/s", 4.0 * m * h * f, step, "fp8_gemm", 2.0 * m * h * f, "mfma", FP8_PEAK_TFLOPS,
             {"workload": "fp8_ffn_m32760_h5120_f13824", "m": m, "hidden": h, "ffn": f,
-             "step": "quant, up GEMM + GELU + row amax, requant, down GEMM + gate-residual"},
+             "step": "quant, up GEMM, GELU-tanh + requant, down GEMM + gate-residual"},
             cpu=cpu)
 
     if wl == "skinny":
@@ -337,24 +420,14 @@ def make_workload(args, dev):
             sets.append(tuple(v.to(dev) for v in (x, codes, scale, b, la, lb)))
         from vflash_amd.fused import fp8_linear_lora
 
-        ex = RowFP8Execution("w8a8", activation_quantizer="hip")
-        fp8_linear_lora(ex, *sets[0])
-
-        fused_pass = kernels.quantize_lora_supported(k, r)
+        scope = ScopeTimer()
+        ex = RowFP8Execution("w8a8", activation_quantizer="hip", measure=scope)
 
         def step(i, timer):
-            xd, cd, sd, bd, ad, bbd = sets[i % len(sets)]
-            # The launches of fused.fp8_linear_lora: one pass for codes, scales and t.
-            if fused_pass:
-                a, sa, tt = kernels.quantize_rows_lora(xd, ad)
-            else:
-                a, sa = kernels.quantize_rows(xd)
-                tt = kernels.lora_down(xd, ad)
-            if timer:
-                timer.start()
-            kernels.fp8_gemm_lora(a, sa, cd, sd, m, tt, bbd, bias=bd)
-            if timer:
-                timer.stop()
+            # The drop-in call fused.fp8_linear_lora (host path included); the
+            # scope hook times its GEMM with the adapter merge.
+            scope.arm(timer)
+            fp8_linear_lora(ex, *sets[i % len(sets)])
 
         # Algorithmic HBM bytes of the whole step: x read once (bf16), codes written
         # and read back (e4m3), row scales, weights (e4m3 + fp32 scale + bf16 bias),
@@ -432,19 +505,22 @@ def make_workload(args, dev):
 
         flops = 2.0 * m * n * k
         if w4a4:
-            return Workload(
+            wlo = Workload(
                 wl, "NVFP4 W4A4 linear TFLOP/s (M=32760,K=5120,N=13824)", "TFLOP/s", flops, step,
                 "nvfp4_gemm_pipe<true>", flops, "mfma", BF16_PEAK_TFLOPS,
                 {"workload": "nvfp4_w4a4_linear_m32760_k5120_n13824", "m": m, "k": k, "n": n,
                  "activations": "NVFP4 (e2m1 + e4m3 block-16 scales, global input scale)",
                  "mfma": "f16 on exactly dequantized e2m1 x e4m3 operands"},
                 dtype="e2m1 x e2m1 with e4m3 block scales (f16 mfma, exact operands)")
-        return Workload(
-            wl, "NVFP4-weight W4A8 linear TFLOP/s (M=32760,K=5120,N=13824)", "TFLOP/s", flops, step,
-            "nvfp4_gemm_pipe<false>", flops, "mfma", BF16_PEAK_TFLOPS,
-            {"workload": "nvfp4_weight_linear_m32760_k5120_n13824", "m": m, "k": k, "n": n,
-             "mfma": "f16 on exactly dequantized e4m3 activations and e2m1 x e4m3 weights"},
-            dtype="e4m3 activations x e2m1 weights (f16 mfma, exact operands)")
+        else:
+            wlo = Workload(
+                wl, "NVFP4-weight W4A8 linear TFLOP/s (M=32760,K=5120,N=13824)", "TFLOP/s", flops, step,
+                "nvfp4_gemm_pipe<false>", flops, "mfma", BF16_PEAK_TFLOPS,
+                {"workload": "nvfp4_weight_linear_m32760_k5120_n13824", "m": m, "k": k, "n": n,
+                 "mfma": "f16 on exactly dequantized e4m3 activations and e2m1 x e4m3 weights"},
+                dtype="e4m3 activations x e2m1 weights (f16 mfma, exact operands)")
+        wlo.fp8_frac = True
+        return wlo
 
     if wl == "norm_quant":
         from vflash_amd.producers import rmsnorm_modulate_quantize
@@ -511,7 +587,7 @@ def make_workload(args, dev):
                     times.append(time.perf_counter() - t0)
                 dt = statistics.median(times)
                 return {"value": nbytes * rows / s_tok / dt / 1e9, "unit": "GB/s", "cores": 1,
-                        "kind": "port",
+                        "threads": 1, "cpu_model": cpu_model(), "kind": "port",
                         "sample": (f"numpy restatement of rms_norm + modulation + per-token quantization "
                                    f"on {rows} of {s_tok} rows, median of 3, {dt * 1e3:.0f} ms")}
 
@@ -561,8 +637,6 @@ def main():
     if not _lib.is_gfx950(dev):
         raise SystemExit("bench.py needs a gfx950 (MI355X) device")
     _lib.library()
-    if args.tile or args.group_m:
-        _lib.set_gemm_tile(args.tile, args.group_m)
 
     w = make_workload(args, dev)
     timer = EventTimer()
@@ -621,6 +695,10 @@ def main():
         },
         "cpu_baseline": w.cpu() if w.cpu is not None else None,
     }
+    if w.fp8_frac:
+        line["roofline"]["frac_of_fp8_peak"] = achieved / FP8_PEAK_TFLOPS
+    if w.cpu_oracle is not None:
+        line["cpu_oracle"] = w.cpu_oracle()
     if w.extra is not None:
         line["unfused_reference_ms_per_step"] = w.extra()
     if w.vendor is not None:

@@ -78,22 +78,26 @@ int vflash_fp8_linear_planes(const void* a, const float* sa, int64_t lda, const 
                              int64_t plane_stride, void* stream);
 
 /*
- * FFN up-projection with a GELU-tanh epilogue.
- * Replaces RowFP8Execution.linear + the FFN activation kernel
- *   (src/vflash/native/h3_native_denoiser.py:369-382; the reference activation
- *   is SiLU-mul at src/vflash/native/h3_fused_ops.py:184-224, GELU-tanh is the
- *   activation of this path's FFN).
- *   g = bf16(gelu_tanh(bf16(bf16(acc * sa * sw) + bias)))  written to g [m, n] (ldg)
- *   amax_part fp32 [m, vflash_row_parts(n)]: max |g| of each row over each
- *   64-column group, consumed by vflash_requant_rows_e4m3.
+ * GELU-tanh of the FFN hidden rows fused with the down linear's per-token E4M3
+ * quantization: the step between the GELU FFN's two linears.
+ * Replaces the FFN activation (the GELU-tanh form of
+ *   src/vflash/native/h3_native_denoiser.py:369-382, whose reference
+ *   activation is SiLU-mul) and the down linear's quantize_activation
+ *   (src/vflash/native/h3_fp8_activation.py:12-55).
+ *   y      bf16 [m, k] (ldy): the up linear's output (vflash_fp8_linear)
+ *   g      = bf16(gelu_tanh(y)), the real function 0.5 y (1 + tanh(u)),
+ *            u = beta (y + kappa y^3) with beta, kappa the binary32 constants of
+ *            sqrt(2/pi) and 0.044715, rounded to binary32 and then to bf16 (a
+ *            table of all 65536 bf16 inputs); written to g [m, k] (ldg) when g is
+ *            not NULL.  +inf gives +inf, -inf NaN, a NaN input stays NaN.
+ *   codes  e4m3 [m_pad, k] contiguous;  scales fp32 [m_pad]: the arithmetic of
+ *          vflash_quantize_rows_e4m3 applied to g.  Rows m..m_pad-1: codes 0, scale 1.
+ *   Requires k % 8 == 0, k <= 16384, ldy and ldg multiples of 8, y and g 16-byte
+ *   aligned, codes 8-byte aligned.
  */
-int vflash_fp8_linear_gelu(const void* a, const float* sa, int64_t lda, const void* w,
-                           const float* sw, int64_t ldw, int64_t m, int64_t n, int64_t k,
-                           const void* bias, void* g, int64_t ldg, float* amax_part,
-                           void* stream);
-
-/* Number of 64-column groups per row in amax_part: ceil(n / 64). */
-int64_t vflash_row_parts(int64_t n);
+int vflash_gelu_quantize_rows_e4m3(const void* y, int64_t m, int64_t k, int64_t ldy, void* g,
+                                   int64_t ldg, void* codes, float* scales, int64_t m_pad,
+                                   void* stream);
 
 /*
  * FFN input projection with the SwiGLU epilogue (the H3 feed-forward input).
@@ -103,7 +107,9 @@ int64_t vflash_row_parts(int64_t n);
  * 660-700).  w holds n = 2F rows: rows [0, F) give the value columns and rows
  * [F, 2F) the gate columns of the packed output, as .chunk(2, dim=-1) splits it.
  *   p   = bf16(bf16(acc * sa * sw) + bias)            (the packed [m, 2F] output)
- *   h   = bf16(p[:, f] * bf16(silu(p[:, F + f])))     written to h [m, F] (ldh)
+ *   h   = bf16(p[:, f] * bf16(silu(p[:, F + f])))     written to h [m, F] (ldh), with
+ *         silu(x) = x / (1 + exp(-x)) evaluated in binary32 with an exponential
+ *         and a quotient each within about one ulp of correctly rounded
  *   amax_part fp32 [m, vflash_swiglu_parts(n)]: max |h| of each row over each
  *   128-column group, consumed by vflash_requant_rows_e4m3.
  *   Requires n % 256 == 0, ldh % 8 == 0, h and sw (and bias) 16-byte aligned.
@@ -232,7 +238,8 @@ int vflash_fp8_linear_lora(const void* a, const float* sa, int64_t lda, const vo
  *            (h3_nvfp4_linear.py:22-33)
  *   alpha    fp32 device scalar (NVFP4Weight.alpha; read on the device, no host sync)
  *   out = bf16(bf16(sum_k a * e2m1(w) * e4m3(s_blk) * sa[m] * alpha) + bias[n])
- *   Requires n % 128 == 0, k % 64 == 0.
+ *   Requires n % 128 == 0, k % 64 == 0, lda % 16 == 0, a, w_packed and w_scales
+ *   16-byte aligned.
  */
 int vflash_nvfp4_linear(const void* a, const float* sa, int64_t lda, const void* w_packed,
                         const void* w_scales, const float* alpha, int64_t m, int64_t n, int64_t k,
@@ -274,29 +281,6 @@ int vflash_nvfp4_quantize_rows(const void* x, int x_is_f16, int64_t m, int64_t k
 int vflash_nvfp4_w4a4_linear(const void* a, int64_t lda, const void* a_scales, const void* w_packed,
                              const void* w_scales, const float* alpha, int64_t m, int64_t n,
                              int64_t k, const void* bias, void* out, int64_t ldo, void* stream);
-
-/*
- * Tuning hook: force a GEMM tile configuration for later calls in this process
- * (0 = automatic, 1 = 256x256, 2 = 128x128, 3 = 64x64, 4 = 128x256, 5 = 256x128,
- * 6 = 256x256 with 8 waves 4x2, 7 = 256x256 with 8 waves 2x4,
- * 10 = 256x256 two-slot 128-byte-stage LDS-DMA pipeline,
- * 12 = 128x128 two-slot pipeline, two workgroups per CU,
- * 13 / 14 = 128x128 with four / three stage slots,
- * 15 = tile 10 with the stage barrier after K-substep 0, 16 = tile 10 with
- * scalar-offset DMA, 17 = both (default for large shapes), 18 = tile 12 with
- * tile 17's schedule, 19 = tile 17 as a persistent grid whose epilogue stores
- * from registers while the next tile's first stages load; other values,
- * including 8, 9 and 11, leave the current configuration unchanged)
- * and the tile-order group height (0 = default: 2 for the E4M3 GEMMs, 8 for the
- * E2M1-weight ones).  The automatic E4M3 choice is 3 below 256 tiles of
- * 128x128, else 17 or 12, whichever needs fewer rounds of tiles over the
- * compute units (a 128x128 round, two workgroups per CU, weighted 0.575 of a
- * 256x256 round).  For vflash_nvfp4_linear the
- * values mean 1 = 256x256, 2 = 128x128, 3 = 64x128 (register-staged) and
- * 4 = 256x256 pipelined (default for large shapes); other values select the
- * automatic choice there.  Returns the previous tile value.
- */
-int vflash_set_gemm_tile(int tile, int group_m);
 
 #ifdef __cplusplus
 }

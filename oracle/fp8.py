@@ -75,31 +75,64 @@ def w8a8_linear(x, w_codes, sw, bias=None):
     return add_bias(scaled_mm(codes[:m], sa[:m], w_codes, sw), bias)
 
 
-def gelu_tanh(y) -> np.ndarray:
-    """bf16(0.5 y (1 + tanh(sqrt(2/pi) (y + 0.044715 y^3)))) in binary32.
+# The binary32 constants a binary32 GELU-tanh kernel multiplies by (torch's
+# gelu(approximate="tanh") forms them as float: sqrt(2) * 2/sqrt(pi) * 0.5 and 0.044715).
+GELU_BETA = float(F32(0.7978845608028654))
+GELU_KAPPA = float(F32(0.044715))
 
-    The reference has no GELU (its FFN is SiLU-mul); this is the textbook tanh
-    approximation, pinned against torch.nn.functional.gelu(approximate="tanh").
-    """
-    y = np.asarray(y, dtype=F32)
-    beta = F32(0.7978845608028654)
-    kappa = F32(0.044715)
-    inner = beta * (y + kappa * y * y * y)
-    return bf16_round(F32(0.5) * y * (F32(1.0) + np.tanh(inner)))
+
+def _bf16_through_f32(v) -> np.ndarray:
+    """Real values (binary64) stored as bf16 by a binary32 kernel: rounded to
+    binary32, then to bf16, each to nearest with ties to even."""
+    with np.errstate(over="ignore"):
+        return bf16_round(np.asarray(v, np.float64).astype(F32))
+
+
+def gelu_tanh(y) -> np.ndarray:
+    """GELU with the tanh approximation, 0.5 y (1 + tanh(u)) with
+    u = beta (y + kappa y^3), of bf16 values, as a binary32 kernel with correctly
+    rounded steps stores it: the function value rounded to binary32, then to
+    bf16.  It is evaluated in binary64 as y / (1 + exp(-2u)), the same function
+    without the cancellation of 1 + tanh(u) at negative y.  +inf gives +inf,
+    -inf gives NaN (-inf * 0 in the tanh form), NaN stays NaN.
+
+    The reference's FFN has no GELU (its activation is SiLU-mul); this is the
+    textbook tanh form of torch.nn.functional.gelu(approximate="tanh").  Pinned
+    against a 60-digit decimal evaluation over every bf16 value and against
+    torch's binary64 gelu (tests/test_oracle_fp8.py)."""
+    y = np.asarray(y, dtype=F32).astype(np.float64)
+    u = GELU_BETA * (y + GELU_KAPPA * y * y * y)
+    with np.errstate(over="ignore", invalid="ignore"):
+        v = y / (1.0 + np.exp(-2.0 * u))
+    return _bf16_through_f32(v)
+
+
+def silu(g) -> np.ndarray:
+    """bf16(silu(g)) of bf16 values: the reference's binary32 formula
+    g / (1 + exp(-g)) (h3_fused_ops.py:205) with each step correctly rounded to
+    binary32 -- e = RN(exp(-g)) (infinity where it overflows, below g = -88.72),
+    d = RN(1 + e), q = RN(g / d) -- then rounded to bf16.  Overflow gives -0 for
+    g <= -89, as the binary32 kernels do; +inf gives +inf, -inf NaN, NaN stays
+    NaN.  Pinned by a 60-digit evaluation of the exponential and against torch's
+    silu (tests/test_oracle_fp8.py)."""
+    g = np.asarray(g, dtype=F32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        e = np.exp(-g.astype(np.float64)).astype(F32)
+        q = g / (F32(1.0) + e)
+    return bf16_round(q)
 
 
 def silu_mul(packed) -> np.ndarray:
     """H3 SwiGLU activation of a packed bf16 [.., 2F] projection output:
-    value, gate = packed.chunk(2, -1); bf16(value * bf16(silu(gate))) with
-    silu(g) = g / (1 + exp(-g)) in binary32 (h3_native_denoiser.py:369-373 with
-    eager bf16 tensors; the fused kernel h3_fused_ops.py:184-224 keeps the same
-    two roundings).  Pinned against torch's eager bf16 value * F.silu(gate)."""
+    value, gate = packed.chunk(2, -1); bf16(value * bf16(silu(gate)))
+    (h3_native_denoiser.py:369-373 with eager bf16 tensors; the fused kernel
+    h3_fused_ops.py:184-224 keeps the same two roundings).  The product of two
+    bf16 values is exact in binary32, so its only rounding is the one to bf16."""
     packed = np.asarray(packed, F32)
     f = packed.shape[-1] // 2
     value, gate = packed[..., :f], packed[..., f:]
-    with np.errstate(over="ignore"):
-        act = bf16_round(gate / (F32(1.0) + np.exp(-gate)))
-        return bf16_round(value * act)
+    with np.errstate(invalid="ignore"):
+        return bf16_round(value.astype(np.float64) * silu(gate).astype(np.float64))
 
 
 def rms_norm(x, weight, eps: float) -> np.ndarray:

@@ -1,9 +1,10 @@
-"""Host-side contract of the drop-in API (mirrors the reference's CPU tests).
+"""Host-side contract of the drop-in modules, checked on the CPU.
 
-Covers tests/test_fp8_linear.py and tests/test_h3_nvfp4_linear.py behaviours:
-weight-only exact expression, module construction, refusal of w8a8 off the
-supported device without counting, layout refusals before any GEMM, observer
-cadence, NVFP4 validation.  No GPU.
+Each test states one clause of the module contract (RowFP8Execution,
+RowFP8Linear, the fused compositions, NVFP4Weight / NVFP4Execution) and checks
+it on small tensors; no GPU is involved.  The fixture data (E4M3 codes
+0..127 as a 16 x 8 matrix, row scales 0.01..0.1) is the one of the reference's
+tests/test_fp8_linear.py:13-16, so the expected values there carry over.
 """
 
 import numpy as np
@@ -15,189 +16,245 @@ from vflash_amd import fused, kernels
 from vflash_amd.fp8_linear import RowFP8Execution, RowFP8Linear, _quantize_activation_torch
 from vflash_amd.nvfp4_linear import NVFP4Execution, NVFP4Weight
 
-
-def weights():
-    codes = torch.arange(128).reshape(16, 8).to(torch.float8_e4m3fn)
-    scales = torch.linspace(0.01, 0.1, 16).unsqueeze(1)
-    return codes, scales
+OUT, IN = 16, 8
 
 
-@pytest.mark.parametrize("shape", [(8,), (3, 8), (2, 3, 8), (0, 8)])
+@pytest.fixture
+def fp8_matrix():
+    """(codes [16, 8] E4M3 holding codes 0..127, row scales [16, 1])."""
+    codes = torch.arange(OUT * IN).reshape(OUT, IN).to(torch.float8_e4m3fn)
+    return codes, torch.linspace(0.01, 0.1, OUT).unsqueeze(1)
+
+
+def restored_linear(value, codes, scales, bias):
+    """The weight-only arithmetic of the contract: restore the weight in the
+    value's dtype from codes * row scale, then an ordinary linear."""
+    return torch.nn.functional.linear(value, (codes.float() * scales).to(value.dtype), bias)
+
+
+# --- weight-only mode: the exact restored-weight expression --------------------
+
+@pytest.mark.parametrize("lead", [(), (3,), (2, 3), (0,)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_weight_only_is_exact_restored_weight_expression(shape, dtype):
-    codes, scales = weights()
-    values = torch.randn(shape, dtype=dtype)
-    bias = torch.randn(16, dtype=dtype)
-    execution = RowFP8Execution()
-    actual = execution.linear(values, codes, scales, bias)
-    restored = (codes.float() * scales).to(dtype)
-    expected = torch.nn.functional.linear(values, restored, bias)
-    torch.testing.assert_close(actual, expected, rtol=0, atol=0)
-    assert execution.calls == {"weight_only": 1, "w8a8": 0}
-
-
-def test_weight_only_golden_vector():
-    g = golden("weight_only_kat.npz")
-    codes = torch.from_numpy(g["codes"]).view(torch.float8_e4m3fn)
-    out = RowFP8Execution().linear(
-        torch.from_numpy(g["values"]).to(torch.bfloat16),
-        codes,
-        torch.from_numpy(g["scales"]),
-        torch.from_numpy(g["bias"]).to(torch.bfloat16),
-    )
-    assert np.array_equal(out.float().numpy(), g["expected"])
-
-
-def test_module_assigns_weight_scales_without_bias_copy():
-    codes, scales = weights()
-    original = torch.nn.Linear(8, 16)
-    execution = RowFP8Execution()
-    module = RowFP8Linear(original, execution)
-    assert module.bias is original.bias and module.weight.is_meta and module.row_scale.is_meta
-    module.load_state_dict({"weight": codes, "row_scale": scales, "bias": original.bias}, assign=True)
-    value = torch.randn(2, 8)
-    torch.testing.assert_close(module(value), execution.linear(value, codes, scales, module.bias), rtol=0, atol=0)
-    assert not module.weight.requires_grad
-
-
-@pytest.mark.parametrize("backend", ["torch", "triton", "hip"])
-def test_w8a8_off_device_fails_without_fallback_or_count(backend):
-    codes, scales = weights()
-    execution = RowFP8Execution("w8a8", activation_quantizer=backend)
-    with pytest.raises(ValueError, match="gfx950"):
-        execution.linear(torch.ones(3, 8, dtype=torch.bfloat16), codes, scales)
-    assert execution.calls == {"weight_only": 0, "w8a8": 0}
-
-
-@pytest.mark.parametrize("bad", ["codes", "scale_dtype", "scale_shape", "input_shape", "rank", "bias"])
-def test_bad_layout_never_enters_gemm(bad, monkeypatch):
-    codes, scales = weights()
-    value = torch.ones(3, 8)
-    bias = None
-    if bad == "codes":
-        codes = codes.float()
-    elif bad == "scale_dtype":
-        scales = scales.bfloat16()
-    elif bad == "scale_shape":
-        scales = scales.T
-    elif bad == "input_shape":
-        value = torch.ones(3, 7)
-    elif bad == "rank":
-        codes = codes.flatten()
-    elif bad == "bias":
-        bias = torch.ones(15)
-
-    def forbidden(*args, **kwargs):
-        pytest.fail("invalid layout reached GEMM")
-
-    monkeypatch.setattr(torch.nn.functional, "linear", forbidden)
-    monkeypatch.setattr(kernels, "fp8_gemm", forbidden)
-    for mode in ("weight-only", "w8a8"):
-        with pytest.raises(ValueError, match="declared"):
-            RowFP8Execution(mode).linear(value, codes, scales, bias)
-
-
-def test_executions_keep_precision_observation_and_counts_independent():
-    codes, scales = weights()
-    a, b = RowFP8Execution(), RowFP8Execution("w8a8")
-    observed = []
-    a.observer = lambda: observed.append(dict(a.calls))
-    a.linear(torch.ones(8), codes, scales)
-    assert observed == [{"weight_only": 0, "w8a8": 0}]
-    assert b.mode == "w8a8" and b.calls == {"weight_only": 0, "w8a8": 0}
-    with pytest.raises(ValueError):
-        a.select("silent-fallback")
-    assert a.mode == "weight-only"
-    with pytest.raises(ValueError):
-        RowFP8Execution(activation_quantizer="cuda")
-    with pytest.raises(ValueError):
-        RowFP8Execution(fast_accum=1)
-
-
-def test_observer_runs_every_200_calls_before_the_call():
-    codes, scales = weights()
+def test_weight_only_output_is_bitwise_the_restored_weight_linear(fp8_matrix, lead, dtype):
+    codes, scales = fp8_matrix
+    gen = torch.Generator().manual_seed(len(lead))
+    value = torch.randn(*lead, IN, generator=gen).to(dtype)
+    bias = torch.randn(OUT, generator=gen).to(dtype)
     ex = RowFP8Execution()
-    seen = []
-    ex.observer = lambda: seen.append(ex.calls["weight_only"])
-    for _ in range(401):
-        ex.linear(torch.ones(8), codes, scales)
-    assert seen == [0, 200, 400]
+    got = ex.linear(value, codes, scales, bias)
+    want = restored_linear(value, codes, scales, bias)
+    assert got.dtype == dtype and got.shape == (*lead, OUT)
+    assert torch.equal(got, want)
+    assert ex.calls == {"weight_only": 1, "w8a8": 0}
 
 
-@pytest.mark.parametrize("rows", [1, 16, 17])
-def test_portable_quantizer_pads_and_keeps_strided_input(rows):
-    base = torch.full((rows, 128), float("nan"), dtype=torch.bfloat16)
-    values = base[:, :64]
-    values.copy_(torch.linspace(-448, 448, 64))
-    values[0].zero_()
-    if rows > 1:
-        values[1].fill_(torch.finfo(torch.bfloat16).tiny)
-    codes, scales = _quantize_activation_torch(values)
-    padded = (rows + 15) // 16 * 16
-    assert codes.shape == (padded, 64) and scales.shape == (padded, 1)
-    assert (codes[0].float() == 0).all() and scales[0].item() == 1
-    assert (codes[rows:].float() == 0).all() and (scales[rows:] == 1).all()
-    assert torch.isnan(base[:, 64:].float()).all()
-    g = golden("quant_kat.npz")
-    assert np.array_equal(codes.view(torch.uint8).numpy(), g[f"codes{rows}"])
+def test_weight_only_matches_the_committed_vector():
+    kat = golden("weight_only_kat.npz")
+    out = RowFP8Execution().linear(
+        torch.from_numpy(kat["values"]).to(torch.bfloat16),
+        torch.from_numpy(kat["codes"]).view(torch.float8_e4m3fn),
+        torch.from_numpy(kat["scales"]),
+        torch.from_numpy(kat["bias"]).to(torch.bfloat16),
+    )
+    assert np.array_equal(out.float().numpy(), kat["expected"])
 
 
-def test_fused_compositions_refuse_before_any_kernel():
-    codes, scales = weights()
-    ex = RowFP8Execution("w8a8")
-    x = torch.ones(3, 8, dtype=torch.bfloat16)
-    with pytest.raises(ValueError, match="gfx950"):
-        fused.qkv_linear(ex, x, torch.cat([codes] * 3), torch.cat([scales] * 3))
-    with pytest.raises(ValueError, match="w8a8"):
-        fused.qkv_linear(RowFP8Execution(), x, codes, scales)
-    with pytest.raises(ValueError, match="matching"):
-        fused.merge_qkv([codes, codes, codes[:8]], [scales] * 3)
+# --- RowFP8Linear: a meta-initialized replacement that keeps the bias object ----
+
+def test_module_starts_on_meta_and_runs_once_assigned(fp8_matrix):
+    codes, scales = fp8_matrix
+    dense = torch.nn.Linear(IN, OUT)
+    ex = RowFP8Execution()
+    mod = RowFP8Linear(dense, ex)
+    # Nothing is materialized before the loader assigns; the bias is the original object.
+    assert mod.weight.is_meta and mod.row_scale.is_meta
+    assert mod.bias is dense.bias
+    assert (mod.in_features, mod.out_features) == (IN, OUT)
+    mod.load_state_dict({"weight": codes, "row_scale": scales, "bias": dense.bias}, assign=True)
+    assert not mod.weight.requires_grad
+    value = torch.randn(2, IN)
+    assert torch.equal(mod(value), ex.linear(value, codes, scales, mod.bias))
+
+
+# --- refusals: each happens before any GEMM and counts nothing ------------------
+
+LAYOUT_BREAKS = {
+    "codes not E4M3": lambda c, s, v, b: (c.float(), s, v, b),
+    "scale not fp32": lambda c, s, v, b: (c, s.bfloat16(), v, b),
+    "scale [1, N] instead of [N, 1]": lambda c, s, v, b: (c, s.T, v, b),
+    "value width differs from K": lambda c, s, v, b: (c, s, torch.ones(3, IN - 1), b),
+    "codes not 2-D": lambda c, s, v, b: (c.flatten(), s, v, b),
+    "bias of the wrong width": lambda c, s, v, b: (c, s, v, torch.ones(OUT - 1)),
+}
+
+
+@pytest.mark.parametrize("mode", ["weight-only", "w8a8"])
+@pytest.mark.parametrize("clause", sorted(LAYOUT_BREAKS))
+def test_layout_refusal_precedes_every_gemm(fp8_matrix, monkeypatch, mode, clause):
+    codes, scales = fp8_matrix
+    args = LAYOUT_BREAKS[clause](codes, scales, torch.ones(3, IN), None)
+
+    def gemm_reached(*_a, **_k):
+        raise AssertionError(f"{clause}: a GEMM ran on a refused layout")
+
+    monkeypatch.setattr(torch.nn.functional, "linear", gemm_reached)
+    monkeypatch.setattr(kernels, "fp8_gemm", gemm_reached)
+    ex = RowFP8Execution(mode)
+    with pytest.raises(ValueError, match="declared"):
+        ex.linear(args[2], args[0], args[1], args[3])
     assert ex.calls == {"weight_only": 0, "w8a8": 0}
 
 
-def nv_weight(scale=4.0):
+@pytest.mark.parametrize("quantizer", ["torch", "triton", "hip"])
+def test_w8a8_without_a_gfx950_device_refuses_with_no_fallback(fp8_matrix, quantizer):
+    codes, scales = fp8_matrix
+    ex = RowFP8Execution("w8a8", activation_quantizer=quantizer)
+    with pytest.raises(ValueError, match="gfx950"):
+        ex.linear(torch.ones(3, IN, dtype=torch.bfloat16), codes, scales)
+    assert ex.calls == {"weight_only": 0, "w8a8": 0}
+
+
+@pytest.mark.parametrize(
+    "build",
+    [
+        lambda: RowFP8Execution("fp16"),
+        lambda: RowFP8Execution(activation_quantizer="cuda"),
+        lambda: RowFP8Execution(fast_accum=1),
+        lambda: RowFP8Execution(fast_accum="yes"),
+    ],
+    ids=["unknown mode", "unknown quantizer", "fast_accum int", "fast_accum str"],
+)
+def test_construction_refuses_undeclared_choices(build):
+    with pytest.raises(ValueError):
+        build()
+
+
+def test_select_refuses_an_unknown_mode_and_keeps_the_current_one():
+    ex = RowFP8Execution()
+    with pytest.raises(ValueError):
+        ex.select("silent-fallback")
+    assert ex.mode == "weight-only"
+    ex.select("w8a8")
+    assert ex.mode == "w8a8"
+
+
+# --- counters and the observer ---------------------------------------------------
+
+def test_each_execution_owns_its_counters_and_observer(fp8_matrix):
+    codes, scales = fp8_matrix
+    first, second = RowFP8Execution(), RowFP8Execution("w8a8")
+    snapshots = []
+    first.observer = lambda: snapshots.append(dict(first.calls))
+    first.linear(torch.ones(IN), codes, scales)
+    # The observer sees the counters before the call it precedes.
+    assert snapshots == [{"weight_only": 0, "w8a8": 0}]
+    assert first.calls == {"weight_only": 1, "w8a8": 0}
+    assert second.mode == "w8a8" and second.calls == {"weight_only": 0, "w8a8": 0}
+    assert second.observer is None
+
+
+def test_observer_fires_on_every_200th_call_ahead_of_it(fp8_matrix):
+    codes, scales = fp8_matrix
+    ex = RowFP8Execution()
+    fired_at = []
+    ex.observer = lambda: fired_at.append(ex.calls["weight_only"])
+    for _ in range(401):
+        ex.linear(torch.ones(IN), codes, scales)
+    assert fired_at == [0, 200, 400]
+
+
+# --- the portable ("torch") activation quantizer ---------------------------------
+
+@pytest.mark.parametrize("rows", [1, 16, 17])
+def test_portable_quantizer_layout_and_known_answers(rows):
+    # Rows are a strided view (every other 64-wide half of a 128-wide buffer);
+    # row 0 is zero (scale 1), row 1 sits at the bf16 minimum normal, the rest
+    # span [-448, 448].
+    storage = torch.full((rows, 2 * 64), float("nan"), dtype=torch.bfloat16)
+    view = storage[:, :64]
+    view.copy_(torch.linspace(-448, 448, 64))
+    view[0].zero_()
+    if rows > 1:
+        view[1].fill_(torch.finfo(torch.bfloat16).tiny)
+    codes, scales = _quantize_activation_torch(view)
+    padded = -(-rows // 16) * 16
+    assert codes.shape == (padded, 64) and scales.shape == (padded, 1)
+    assert scales[0].item() == 1.0 and not codes[0].view(torch.uint8).any()
+    # Padding rows: codes 0, scale 1.
+    assert not codes[rows:].view(torch.uint8).any() and bool((scales[rows:] == 1).all())
+    # The input's other half is untouched.
+    assert bool(torch.isnan(storage[:, 64:].float()).all())
+    assert np.array_equal(codes.view(torch.uint8).numpy(), golden("quant_kat.npz")[f"codes{rows}"])
+
+
+# --- fused compositions refuse exactly like the linear ---------------------------
+
+def test_fused_compositions_refuse_before_any_kernel(fp8_matrix):
+    codes, scales = fp8_matrix
+    ex = RowFP8Execution("w8a8")
+    x = torch.ones(3, IN, dtype=torch.bfloat16)
+    merged = torch.cat([codes] * 3), torch.cat([scales] * 3)
+    with pytest.raises(ValueError, match="gfx950"):
+        fused.qkv_linear(ex, x, *merged)
+    with pytest.raises(ValueError, match="w8a8"):
+        fused.qkv_linear(RowFP8Execution(), x, codes, scales)
+    with pytest.raises(ValueError, match="matching"):
+        fused.merge_qkv([codes, codes, codes[: OUT // 2]], [scales] * 3)
+    assert ex.calls == {"weight_only": 0, "w8a8": 0}
+
+
+# --- NVFP4 ----------------------------------------------------------------------
+
+def nvfp4(rows=128, half_k=32, scale_cols=4, alpha=2.0, input_scale=4.0):
     return NVFP4Weight(
-        torch.zeros((128, 32), dtype=torch.uint8),
-        torch.zeros((128, 4), dtype=torch.uint8),
-        torch.tensor(2.0, dtype=torch.float32),
-        torch.tensor(scale, dtype=torch.float32),
+        torch.zeros((rows, half_k), dtype=torch.uint8),
+        torch.zeros((rows, scale_cols), dtype=torch.uint8),
+        torch.tensor(alpha, dtype=torch.float32),
+        torch.tensor(input_scale, dtype=torch.float32),
     )
 
 
-@pytest.mark.parametrize("scale", [0.0, -1.0, float("nan"), float("inf")])
-def test_nvfp4_invalid_calibration_cannot_become_a_valid_model(scale):
+@pytest.mark.parametrize("bad", [0.0, -1.0, float("nan"), float("inf")])
+@pytest.mark.parametrize("which", ["alpha", "input_scale"])
+def test_nvfp4_calibration_must_be_positive_and_finite(which, bad):
     with pytest.raises(ValueError, match="positive and finite"):
-        nv_weight(scale)
+        nvfp4(**{which: bad})
 
 
-def test_nvfp4_layout_refusals():
+@pytest.mark.parametrize(
+    "shape", [dict(rows=100), dict(scale_cols=3), dict(half_k=30, scale_cols=3)],
+    ids=["rows not a multiple of 128", "scales not K/16", "K/2 not a multiple of 32"],
+)
+def test_nvfp4_layout_must_be_the_128x4_contract(shape):
     with pytest.raises(ValueError, match="128x4"):
-        NVFP4Weight(torch.zeros((100, 32), dtype=torch.uint8), torch.zeros((100, 4), dtype=torch.uint8),
-                    torch.tensor(1.0), torch.tensor(1.0))
-    with pytest.raises(ValueError, match="128x4"):
-        NVFP4Weight(torch.zeros((128, 32), dtype=torch.uint8), torch.zeros((128, 3), dtype=torch.uint8),
-                    torch.tensor(1.0), torch.tensor(1.0))
+        nvfp4(**shape)
 
 
-def test_nvfp4_unsupported_device_refuses_and_counts_nothing():
+@pytest.mark.parametrize(
+    "value,match",
+    [
+        (torch.ones((1, 64), dtype=torch.bfloat16), "gfx950"),
+        (torch.ones((1, 63), dtype=torch.bfloat16), "frozen"),
+        (torch.ones((1, 64), requires_grad=True), "inference-only"),
+    ],
+    ids=["no gfx950 device", "width differs", "needs grad"],
+)
+def test_nvfp4_refusals_count_nothing(value, match):
     ex = NVFP4Execution()
-    with pytest.raises(ValueError, match="gfx950"):
-        ex.linear(torch.ones((1, 64), dtype=torch.bfloat16), nv_weight())
-    with pytest.raises(ValueError, match="frozen"):
-        ex.linear(torch.ones((1, 63), dtype=torch.bfloat16), nv_weight())
-    with pytest.raises(ValueError, match="inference-only"):
-        ex.linear(torch.ones((1, 64), requires_grad=True), nv_weight())
-    assert ex.calls == 0 and ex.rows == 0
+    with pytest.raises(ValueError, match=match):
+        ex.linear(value, nvfp4())
+    assert (ex.calls, ex.rows) == (0, 0)
 
 
-def test_bench_measures_one_gpu_only():
-    # This path is measured on one MI355X; several GPUs are a design note.
+# --- measurement ---------------------------------------------------------------
+
+def test_bench_refuses_more_than_one_gpu():
     import subprocess
     import sys
     from pathlib import Path
 
-    root = Path(__file__).resolve().parents[1]
-    result = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"],
-                            capture_output=True, text=True, timeout=120)
-    assert result.returncode != 0
-    assert "one GPU" in result.stderr + result.stdout
+    bench = Path(__file__).resolve().parents[1] / "bench.py"
+    done = subprocess.run([sys.executable, str(bench), "--gpus", "2"], capture_output=True,
+                          text=True, timeout=120)
+    assert done.returncode != 0 and "one GPU" in done.stderr + done.stdout

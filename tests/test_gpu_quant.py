@@ -89,12 +89,14 @@ def test_strided_input_is_read_not_written(dev):
     assert torch.isnan(base[:, 512:].float()).all()
 
 
-def test_matches_portable_torch_expression_on_device(dev):
+def test_matches_the_portable_expression_where_torch_divides(dev):
+    # torch's CPU kernels evaluate amax / 448.0 as a division, the fused
+    # quantizer's arithmetic: same codes and scales, bit for bit.
     g = torch.Generator().manual_seed(0)
-    x = torch.randn((4096, 3072), generator=g).to(torch.bfloat16).to(dev)
-    c1, s1 = quantize_activation(x)
+    x = torch.randn((4096, 3072), generator=g).to(torch.bfloat16)
+    c1, s1 = quantize_activation(x.to(dev))
     c2, s2 = _quantize_activation_torch(x)
-    assert torch.equal(c1.view(torch.uint8), c2.view(torch.uint8)) and torch.equal(s1, s2)
+    assert torch.equal(c1.view(torch.uint8).cpu(), c2.view(torch.uint8)) and torch.equal(s1.cpu(), s2)
 
 
 def test_metric_shape_sampled_rows_and_full_properties(dev):
@@ -218,8 +220,8 @@ def test_non_finite_rows_follow_torch(dev, k):
     codes, scales = kernels.quantize_rows(x.to(dev))  # k = 200: the generic kernel
     assert_codes_like_torch(codes, scales, x)
     if k % 16 == 0:
-        ref_c, ref_s = _quantize_activation_torch(x.to(dev))
-        assert torch.equal(scales, ref_s)
+        ref_c, ref_s = _quantize_activation_torch(x)  # torch's CPU kernels divide, as the kernel does
+        assert torch.equal(scales.cpu(), ref_s)
 
 
 def test_non_finite_rows_in_the_fused_quantizers(dev):
@@ -241,8 +243,9 @@ def test_non_finite_rows_in_the_fused_quantizers(dev):
 
 
 def test_requantization_after_a_nan_row(dev):
-    # A NaN input row makes the whole GELU output row NaN; its requantization
-    # must give NaN codes with scale 1 (torch's amax), not finite codes.
+    # A NaN input row makes the whole up-projection row NaN, and its GELU; the
+    # requantization must give NaN codes with scale 1 (torch's amax), not
+    # finite codes.
     from vflash_amd.prepare import quantize_weight_rows
 
     m, h, f = 32, 256, 512
@@ -251,8 +254,83 @@ def test_requantization_after_a_nan_row(dev):
     x[5, 7] = float("nan")
     cu, su = quantize_weight_rows(torch.randn((f, h), generator=g) * 0.02)
     a, sa = kernels.quantize_rows(x.to(dev))
-    gg, amax = kernels.fp8_gemm_gelu(a, sa, cu.to(dev), su.to(dev), m)
-    assert torch.isnan(amax[5]).all() and not torch.isnan(amax[torch.arange(m) != 5]).any()
-    hc, hs = kernels.requant_rows(gg, amax)
+    y = kernels.fp8_gemm(a, sa, cu.to(dev), su.to(dev), m)
+    hc, hs, gg = kernels.gelu_quantize_rows(y, keep_values=True)
+    assert torch.isnan(gg[5].float()).all() and not torch.isnan(gg[torch.arange(m) != 5].float()).any()
     assert_codes_like_torch(hc, hs, gg.cpu())
     assert hs[5].item() == 1.0
+
+
+def test_gelu_table_on_every_bf16_value(dev):
+    # Every bf16 pattern (inf, NaN and subnormals included) through the GELU
+    # quantizer: g is the oracle's correctly rounded GELU-tanh, bit for bit.
+    from oracle import fp8 as O
+    from oracle.formats import bf16_from_bits
+
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    y = bits.reshape(64, 1024).to(dev)
+    _, _, g = kernels.gelu_quantize_rows(y, keep_values=True)
+    got = g.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+    want = O.gelu_tanh(bf16_from_bits(np.arange(65536, dtype=np.uint32).astype(np.uint16)))
+    want_bits = (want.view(np.uint32) >> 16).astype(np.uint16)
+    nan = np.isnan(want)
+    assert np.array_equal(got[~nan], want_bits[~nan])
+    # NaN inputs stay NaN with their sign; -inf gives NaN.
+    assert np.all((got[nan] & 0x7F80) == 0x7F80) and np.all(got[nan] & 0x7F)
+    src = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    nan_in = ((src & 0x7F80) == 0x7F80) & ((src & 0x7F) != 0)
+    assert np.array_equal(got[nan_in] & 0x8000, src[nan_in] & 0x8000)
+
+
+def test_silu_epilogue_on_every_bf16_gate_value(dev):
+    # The SwiGLU epilogue's silu (binary32 exponential and quotient within about
+    # one ulp of correctly rounded) against the oracle's correctly rounded steps
+    # over every finite bf16 gate value.  Zero activations and weights make the
+    # GEMM's output its bias exactly: the value columns carry 1.0 and the gate
+    # columns every gate value, so h = bf16(1 * bf16(silu(g))) = bf16(silu(g)).
+    from oracle import fp8 as O
+    from oracle.formats import bf16_from_bits
+
+    gates = bf16_from_bits(np.arange(65536, dtype=np.uint32).astype(np.uint16))
+    gates = gates[np.isfinite(gates) & ~((gates == 0) & np.signbit(gates))]  # +0 + -0 is +0
+    f = -(-gates.size // 128) * 128
+    gate_cols = np.zeros(f, np.float32)
+    gate_cols[: gates.size] = gates
+    bias = torch.from_numpy(np.concatenate([np.ones(f, np.float32), gate_cols])).to(torch.bfloat16)
+    m, k = 16, 64
+    a = torch.zeros((m, k), dtype=torch.float8_e4m3fn, device=dev)
+    sa = torch.ones((m, 1), dtype=torch.float32, device=dev)
+    w = torch.zeros((2 * f, k), dtype=torch.float8_e4m3fn, device=dev)
+    sw = torch.ones((2 * f, 1), dtype=torch.float32, device=dev)
+    h, _ = kernels.fp8_gemm_swiglu(a, sa, w, sw, m, bias.to(dev))
+    got = h.float().cpu().numpy()
+    assert np.array_equal(got[0], got[m - 1])
+    got = got[0, : gates.size]
+    want = O.silu(gates)
+    differ = got.view(np.uint32) != want.view(np.uint32)
+    print(f"silu epilogue: {int(differ.sum())} of {gates.size} gate values differ from the oracle "
+          f"(all within one bf16 step: {bool(np.all(np.abs(got - want)[differ] <= np.abs(want[differ]) * 2.0**-7 + 2.0**-133))})")
+    assert np.all(np.abs(got - want) <= np.abs(want) * 2.0**-7 + 2.0**-133)
+    assert int(differ.sum()) <= 2
+
+
+
+def test_portable_mode_keeps_torchs_scalar_division_on_the_gpu(dev):
+    # One row per positive finite bf16 maximum.  The portable ("torch") mode is
+    # the reference's expression amax / 448.0, which torch's GPU kernels
+    # evaluate as amax * RN(1/448); the fused quantizer divides (IEEE), as the
+    # reference's Triton kernel does with div_rn.  The two scales differ by one
+    # ulp in 17410 of the 32639 maxima, and nowhere else.
+    maxima = bf16_from_bits(np.arange(0x0001, 0x7F80, dtype=np.uint32).astype(np.uint16))
+    x = np.zeros((maxima.size, 16), np.float32)
+    x[:, 3] = maxima
+    xd = torch.from_numpy(x).to(torch.bfloat16).to(dev)
+    _, portable = _quantize_activation_torch(xd)
+    _, fused = kernels.quantize_rows(xd)
+    tiny = np.float32(np.finfo(np.float32).tiny)
+    product = np.maximum((maxima * (np.float32(1.0) / np.float32(448.0))).astype(np.float32), tiny)
+    quotient = np.maximum((maxima / np.float32(448.0)).astype(np.float32), tiny)
+    rows = maxima.size
+    assert np.array_equal(portable.reshape(-1)[:rows].cpu().numpy().view(np.uint32), product.view(np.uint32))
+    assert np.array_equal(fused.reshape(-1)[:rows].cpu().numpy().view(np.uint32), quotient.view(np.uint32))
+    assert int((product != quotient).sum()) == 17410

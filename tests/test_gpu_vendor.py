@@ -88,7 +88,7 @@ def reference_ffn(x, cu, su, bu, cd, sd, bd, gate, res, activation):
     codes and row scales, and |residual| + |gate * z| (the magnitude of the
     final sum's addends)."""
     m = x.shape[0]
-    a, sa = kernels.quantize_rows(x)  # bit-identical to _quantize_activation_torch
+    a, sa = kernels.quantize_rows(x)  # the fused quantizer, the arithmetic of the reference's Triton kernel
     y = reference_call(a, sa, cu, su, bu, m)
     if activation == "swiglu":
         value, g = y.chunk(2, dim=-1)
@@ -122,16 +122,22 @@ def test_ffn_matches_the_reference_composition(dev, activation, m, h, f):
     ours = fp8_ffn(ex, *t, activation=activation)
     # The same launches staged, to read the down linear's input codes and scales.
     a, sa = kernels.quantize_rows(xd)
-    up = kernels.fp8_gemm_swiglu if activation == "swiglu" else kernels.fp8_gemm_gelu
-    hh, amax = up(a, sa, cud, sud, m, bud)
-    hc, hs = kernels.requant_rows(hh, amax)
+    if activation == "swiglu":
+        hh, amax = kernels.fp8_gemm_swiglu(a, sa, cud, sud, m, bud)
+        hc, hs = kernels.requant_rows(hh, amax)
+        del amax
+    else:
+        hh = kernels.fp8_gemm(a, sa, cud, sud, m, bud)
+        hc, hs, _ = kernels.gelu_quantize_rows(hh)
     assert torch.equal(kernels.fp8_gemm_gate_residual(hc, hs, cdd, sdd, m, gated, resd, bdd), ours)
     ref, ref_hc, ref_hs, addends = reference_ffn(*t, activation)
-    del hh, amax, a, sa
-    # Error model.  The activation rounds one bf16 step away from torch's in a
-    # few per mille of the hidden elements (hardware exp and reciprocal against
-    # torch's kernels).  Requantization turns such a step into a re-rounded
-    # E4M3 code, or, at a row's maximum, a new row scale.  Those input
+    del hh, a, sa
+    # Error model.  The hidden activations differ from torch's where the two
+    # up-projection sums round apart (about 1e-5 of the outputs) and where
+    # torch's binary32 activation is not correctly rounded: its GELU loses
+    # digits where 1 + tanh(u) cancels (y below about -2), and its exp and
+    # quotient round within an ulp or so.  Requantization turns such a bf16 step
+    # into a re-rounded E4M3 code, or, at a row's maximum, a new row scale.  Those input
     # differences reach z through the down weights exactly:
     #   |dz| <= (|dequant(ours) - dequant(ref)| . |W_down|^T) * s_down,
     # and z enters the output as gate * z.  Beyond that propagated bound, the
@@ -154,7 +160,10 @@ def test_ffn_matches_the_reference_composition(dev, activation, m, h, f):
     print(f"[{activation} {m}x{h}x{f}] identical {exact:.5f}; requantization codes differing "
           f"{codes_moved:.2e} (in {rows_moved:.3f} of the rows); max (|diff| - propagated) / "
           f"(addends + rms) {float((slack / (addends + rms)).max()):.3g}")
-    assert exact > 0.9 and codes_moved < 1e-3
+    # Measured at the full shape: 1.69e-5 (GELU: torch's binary32 1 + tanh(u)
+    # cancels at negative inputs, where the kernel's correctly rounded GELU
+    # differs from it) and 6.4e-7 (SwiGLU).
+    assert exact > 0.9 and codes_moved < (2e-5 if activation == "gelu_tanh" else 1e-6)
 
 
 def test_merged_qkv_planes_match_the_reference_call(dev):

@@ -28,18 +28,13 @@ _F32 = ctypes.c_float
 SIGNATURES: dict[str, tuple[list, object]] = {
     "vflash_abi_version": ([], _I32),
     "vflash_status_string": ([_I32], ctypes.c_char_p),
-    "vflash_set_gemm_tile": ([_I32, _I32], _I32),
     "vflash_quantize_rows_e4m3": ([_P, _I64, _I64, _I64, _P, _P, _I64, _P], _I32),
     "vflash_fp8_linear": ([_P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P], _I32),
     "vflash_fp8_linear_planes": (
         [_P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _P],
         _I32,
     ),
-    "vflash_fp8_linear_gelu": (
-        [_P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _P],
-        _I32,
-    ),
-    "vflash_row_parts": ([_I64], _I64),
+    "vflash_gelu_quantize_rows_e4m3": ([_P, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P], _I32),
     "vflash_fp8_linear_swiglu": (
         [_P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _P],
         _I32,
@@ -90,7 +85,7 @@ def library() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = restype
-    if lib.vflash_abi_version() != 2:
+    if lib.vflash_abi_version() != 3:
         raise RuntimeError("libvflash_amd.so has an unexpected ABI version")
     return lib
 
@@ -145,8 +140,3 @@ def stream_of(device: torch.device) -> int:
 def ptr(tensor: torch.Tensor | None) -> int | None:
     """Device address of a tensor's first element, or None (NULL) for an absent operand."""
     return None if tensor is None else tensor.data_ptr()
-
-
-def set_gemm_tile(tile: int, group_m: int = 0) -> int:
-    """Force a GEMM tile configuration (0 = automatic); returns the previous one."""
-    return library().vflash_set_gemm_tile(tile, group_m)

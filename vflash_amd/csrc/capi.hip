@@ -14,6 +14,8 @@ namespace vfa {
 hipError_t launch_quant_rows(const uint16_t*, int64_t, int64_t, int64_t, uint8_t*, float*,
                              int64_t, hipStream_t);
 hipError_t launch_norm_mod_quant(const NormModParams&, hipStream_t);
+hipError_t launch_gelu_quant_rows(const uint16_t*, int64_t, int64_t, int64_t, uint16_t*, int64_t,
+                                  uint8_t*, float*, int64_t, hipStream_t);
 hipError_t launch_requant_rows(const uint16_t*, int64_t, int64_t, int64_t, const float*, int,
                                uint8_t*, float*, int64_t, hipStream_t);
 hipError_t launch_fp8_gemm(const GemmParams&, int, hipStream_t);
@@ -27,18 +29,16 @@ hipError_t launch_nvfp4_w4a4(const uint8_t*, int64_t, const uint8_t*, const uint
                              const uint8_t*, const float*, int64_t, int64_t, int64_t,
                              const uint16_t*, uint16_t*, int64_t, int, hipStream_t);
 hipError_t launch_nvfp4(const uint8_t*, const float*, int64_t, const uint8_t*, const uint8_t*,
-                        const float*, int64_t, int64_t, int64_t, const uint16_t*, uint16_t*, int64_t, int,
+                        const float*, int64_t, int64_t, int64_t, const uint16_t*, uint16_t*, int64_t,
                         int, hipStream_t);
 }  // namespace vfa
 
 namespace {
 
-int g_tile = 0;     // tuning override (0 = automatic)
-// Tile-order group height (0 = automatic: 2 for the E4M3 GEMMs and 8 for the
-// E2M1-weight GEMM, the fastest of a sweep over 1..32 at the large shapes).
-int g_group_m = 0;
-int fp8_group_m() { return g_group_m > 0 ? g_group_m : 2; }
-int fp4_group_m() { return g_group_m > 0 ? g_group_m : 8; }
+// Tile-order group heights: 2 for the E4M3 GEMMs and 8 for the E2M1-weight
+// GEMMs, the fastest of a sweep over 1..32 at the large shapes.
+constexpr int FP8_GROUP_M = 2;
+constexpr int FP4_GROUP_M = 8;
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
@@ -77,8 +77,7 @@ vfa::GemmParams base_params(const void* a, const float* sa, int64_t lda, const v
   p.ldo = ldo;
   p.lora_scale = 1.0f;
   p.lora_strength = 1.0f;
-  p.group_m = fp8_group_m();
-  p.tile = g_tile;
+  p.group_m = FP8_GROUP_M;
   return p;
 }
 
@@ -86,7 +85,7 @@ vfa::GemmParams base_params(const void* a, const float* sa, int64_t lda, const v
 
 extern "C" {
 
-int vflash_abi_version(void) { return 2; }
+int vflash_abi_version(void) { return 3; }
 
 const char* vflash_status_string(int s) {
   switch (s) {
@@ -95,13 +94,6 @@ const char* vflash_status_string(int s) {
     case VFLASH_ELAUNCH: return "HIP launch failed";
     default: return "unknown status";
   }
-}
-
-int vflash_set_gemm_tile(int tile, int group_m) {
-  const int prev = g_tile;
-  if (tile >= 0 && tile <= 19 && tile != 8 && tile != 9 && tile != 11) g_tile = tile;
-  g_group_m = group_m > 0 ? group_m : 0;
-  return prev;
 }
 
 int vflash_quantize_rows_e4m3(const void* x, int64_t m, int64_t k, int64_t ldx, void* codes,
@@ -135,20 +127,6 @@ int vflash_fp8_linear_planes(const void* a, const float* sa, int64_t lda, const 
   p.plane_cols = plane_cols;
   p.plane_stride = plane_stride;
   return status(vfa::launch_fp8_gemm(p, vfa::EPI_BIAS, static_cast<hipStream_t>(stream)));
-}
-
-int64_t vflash_row_parts(int64_t n) { return n > 0 ? (n + 63) / 64 : 0; }
-
-int vflash_fp8_linear_gelu(const void* a, const float* sa, int64_t lda, const void* w,
-                           const float* sw, int64_t ldw, int64_t m, int64_t n, int64_t k,
-                           const void* bias, void* g, int64_t ldg, float* amax_part,
-                           void* stream) {
-  if (!gemm_args_ok(a, sa, lda, w, sw, ldw, m, n, k, bias)) return VFLASH_EINVAL;
-  if (!g || !amax_part || ldg < n || ldg % 4 || !aligned(g, 8) || !aligned(amax_part, 4))
-    return VFLASH_EINVAL;
-  vfa::GemmParams p = base_params(a, sa, lda, w, sw, ldw, m, n, k, bias, g, ldg);
-  p.amax_part = amax_part;
-  return status(vfa::launch_fp8_gemm(p, vfa::EPI_GELU, static_cast<hipStream_t>(stream)));
 }
 
 int64_t vflash_swiglu_parts(int64_t n) { return n > 0 ? (n / 2 + 127) / 128 : 0; }
@@ -204,6 +182,21 @@ int vflash_rmsnorm_modulate_quantize_e4m3(const void* x, int64_t m, int64_t k, i
   p.scales = scales;
   p.m_pad = m_pad;
   return status(vfa::launch_norm_mod_quant(p, static_cast<hipStream_t>(stream)));
+}
+
+int vflash_gelu_quantize_rows_e4m3(const void* y, int64_t m, int64_t k, int64_t ldy, void* g,
+                                   int64_t ldg, void* codes, float* scales, int64_t m_pad,
+                                   void* stream) {
+  if (!y || !codes || !scales || m < 1 || k < 8 || k > 16384 || k % 8 || m_pad < m)
+    return VFLASH_EINVAL;
+  if (ldy < k || ldy % 8 || !aligned(y, 16) || !aligned(codes, 8) || !aligned(scales, 4))
+    return VFLASH_EINVAL;
+  if (g && (ldg < k || ldg % 8 || !aligned(g, 16))) return VFLASH_EINVAL;
+  if (m_pad >= (int64_t(1) << 33)) return VFLASH_EINVAL;
+  return status(vfa::launch_gelu_quant_rows(static_cast<const uint16_t*>(y), m, k, ldy,
+                                            static_cast<uint16_t*>(g), ldg,
+                                            static_cast<uint8_t*>(codes), scales, m_pad,
+                                            static_cast<hipStream_t>(stream)));
 }
 
 int vflash_requant_rows_e4m3(const void* g, int64_t m, int64_t k, int64_t ldg,
@@ -297,20 +290,16 @@ int vflash_nvfp4_linear(const void* a, const float* sa, int64_t lda, const void*
   if (!a || !sa || !w_packed || !w_scales || !alpha || !out || m < 1 || n < 128 || k < 64)
     return VFLASH_EINVAL;
   if (n % 128 || k % 64 || lda < k || lda % 16 || ldo < n || ldo % 4) return VFLASH_EINVAL;
-  if (!aligned(a, 16) || !aligned(w_packed, 16) || !aligned(w_scales, 2) || !aligned(out, 8))
+  if (!aligned(a, 16) || !aligned(w_packed, 16) || !aligned(w_scales, 16) || !aligned(out, 8))
     return VFLASH_EINVAL;
   if (bias && !aligned(bias, 2)) return VFLASH_EINVAL;
-  if (!aligned(alpha, 4)) return VFLASH_EINVAL;
+  if (!aligned(alpha, 4) || !aligned(sa, 4)) return VFLASH_EINVAL;
   if (256 * lda >= (int64_t(1) << 31)) return VFLASH_EINVAL;
-  int tile = (g_tile >= 1 && g_tile <= 4) ? g_tile : 0;
-  // The pipelined kernel copies block scales with 16-byte DMA; other alignments
-  // use the register-staged kernels.
-  if (!aligned(w_scales, 16) && (tile == 0 || tile == 4)) tile = 2;
   return status(vfa::launch_nvfp4(static_cast<const uint8_t*>(a), sa, lda,
                                   static_cast<const uint8_t*>(w_packed),
                                   static_cast<const uint8_t*>(w_scales), alpha, m, n, k,
                                   static_cast<const uint16_t*>(bias),
-                                  static_cast<uint16_t*>(out), ldo, tile, fp4_group_m(),
+                                  static_cast<uint16_t*>(out), ldo, FP4_GROUP_M,
                                   static_cast<hipStream_t>(stream)));
 }
 
@@ -342,7 +331,7 @@ int vflash_nvfp4_w4a4_linear(const void* a, int64_t lda, const void* a_scales, c
   return status(vfa::launch_nvfp4_w4a4(
       static_cast<const uint8_t*>(a), lda, static_cast<const uint8_t*>(a_scales),
       static_cast<const uint8_t*>(w_packed), static_cast<const uint8_t*>(w_scales), alpha, m, n, k,
-      static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(out), ldo, fp4_group_m(),
+      static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(out), ldo, FP4_GROUP_M,
       static_cast<hipStream_t>(stream)));
 }
 

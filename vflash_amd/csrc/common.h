@@ -138,8 +138,9 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint32_t lds
 
 // lds_dma16 with a scalar byte offset added to the lane offset (soffset): the
 // K advance of a stage then costs no vector instruction.  The resource's range
-// check is applied to the lane offset (callers keep lane offset + soffset
-// inside the same buffer row whenever the lane offset is in range).
+// check covers the lane offset only, not soffset, so it no longer protects the
+// bytes soffset reaches: callers use this form only where every lane offset +
+// soffset they form lies inside the operand (the GEMM's full tiles).
 __device__ __forceinline__ void lds_dma16_so(__amdgpu_buffer_rsrc_t r, uint32_t lds_dst,
                                              uint32_t voffset, uint32_t soffset) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
@@ -198,15 +199,41 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// tanh-approximated GELU in binary32: 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3),
-// evaluated as x * sigmoid(2u) = x / (1 + exp(-2u)), which is the same function
-// with no cancellation for large negative x; exp and the reciprocal use the
-// hardware v_exp_f32 / v_rcp_f32 (about one binary32 ulp each).
-__device__ __forceinline__ float gelu_tanh(float x) {
-  const float two_beta_log2e = 2.0f * 0.7978845608028654f * 1.4426950408889634f;
-  const float kappa = 0.044715f;
-  const float z = -two_beta_log2e * (x + kappa * x * x * x);
-  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z));
+// silu(g) = g / (1 + exp(-g)) in binary32 for a bf16 value g, the formula of
+// the reference's SwiGLU kernel (h3_fused_ops.py:205) with each step close to
+// correctly rounded:
+//   exp(-g) = 2^t, t = -g log2(e).  log2(e) = L_HI + L_LO with L_HI of 16
+//     significant bits, so t_hi = -g L_HI is exact (g has at most 8); with
+//     n = rint(t_hi), a = (t_hi - n) + (-g L_LO) is the reduced argument to
+//     about 2^-26 (t_hi - n is exact), and e = 2^n * v_exp_f32(a) is within
+//     about one binary32 ulp of exp(-g) (Cody and Waite's additive range
+//     reduction; v_exp_f32 is accurate to one ulp on |a| <= 0.5).  t_hi is
+//     clamped to +-200, past which 2^t over- or underflows binary32 anyway.
+//   d = 1 + e, then q = g / d by Markstein's correction of the hardware
+//     reciprocal y: q0 = g y, r = g - q0 d (exact), q = q0 + r y, with the
+//     residual formed negated, r' = q0 d - g and q = q0 + r' (-y): the same
+//     value, and a zero quotient keeps the sign of g.  The hardware
+//     reciprocal flushes results below 2^-126 to zero, so where e >= 2^63
+//     (g <= -44) both g and d are scaled by 2^-64 first: d 2^-64 is formed as
+//     2^-64 + e 2^-64, which rounds exactly as 1 + e does, and g 2^-64 is exact.
+// Where r is NaN the quotient is a special case that q0 already holds:
+// g = +inf gives +inf, g = -inf or NaN gives NaN, and d = inf (exp(-g)
+// overflows for g <= -89) gives -0 -- the binary32 formula's own results.
+__device__ __forceinline__ float silu_of_bf16(float g) {
+  constexpr float L_HI = 1.44268798828125f;      // 47274 / 2^15
+  constexpr float L_LO = 7.0526075433008373e-06f;  // log2(e) - L_HI
+  const float th = __builtin_amdgcn_fmed3f(-g * L_HI, -200.0f, 200.0f);
+  const float n = __builtin_rintf(th);
+  const float a = __builtin_fmaf(-g, L_LO, th - n);
+  const float sc = n >= 63.0f ? 0x1p-64f : 1.0f;
+  const float e = __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f(a), (int)n) * sc;
+  const float d = sc + e;
+  const float gs = g * sc;
+  const float y = __builtin_amdgcn_rcpf(d);
+  const float q0 = gs * y;
+  const float r = __builtin_fmaf(q0, d, -gs);
+  const float q = __builtin_fmaf(r, -y, q0);
+  return r == r ? q : q0;
 }
 
 // E2M1 (OCP MX): bit 3 sign, bits 2..1 exponent (bias 1), bit 0 mantissa.

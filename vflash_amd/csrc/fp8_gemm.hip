@@ -8,8 +8,6 @@
 // (reference src/vflash/native/h3_fp8_linear.py:109-121); the two bf16
 // roundings are kept in that order.  Epilogue variants:
 //   EPI_BIAS   out = base                                   (also merged QKV planes)
-//   EPI_GELU   out = bf16(gelu_tanh(base)), plus per-row |out| maxima per
-//              64-column group for the following requantization
 //   EPI_GATE   out = bf16(residual + bf16(gate * base))
 //              (h3_fused_ops.py:124-170 strict_gate_residual_kernel)
 //   EPI_LORA   out = bf16(base + delta), delta = bf16(t . B^T) with the optional
@@ -170,24 +168,13 @@ constexpr int PIPE2_LDS = pipe2_lds(256);  // two 64 KB stage slots
 // so NS - 1 stages are in flight while one is multiplied.
 // PRE: MFMAs of K-substep 1 issued before the stage barrier (-1: half of them);
 // the DMA of the next stage is spread over the remaining ones.
-// SDMA: K % 128 == 0; the DMA advances K through the scalar offset and kills
-// stages past the end by switching to an empty buffer resource, so issuing a
-// DMA instruction costs no vector instruction.
-// PERSIST (EPI_BIAS, 256x256, two slots, SDMA): one tile of a persistent
-// workgroup.  The epilogue stores straight from registers (direct_epilogue),
-// so the ring is free once the main loop ends: when `has_next`, the scale/bias
-// vectors of tile (tm2, tn2) (into the other vector buffer, vec_lds2) and its
-// stages 0 and 1 are issued before this tile's 32 stores per wave.  Vector
-// memory operations complete in issue order, so the next tile waits for stage
-// 0 with vmcnt <= DMA + 32 and for stage 1 with vmcnt <= 32, and the stores
-// drain behind its first MFMAs; `first` tiles issue their own vectors and
-// stages and wait as the non-persistent form does.
-template <int EPI, int BT = 256, int NS = 2, int PRE = -1, bool SDMA = false, bool PERSIST = false>
+// SDMA: K % 128 == 0; in full tiles the DMA advances K through the scalar
+// offset and kills stages past the end by switching to an empty buffer
+// resource, so issuing a DMA instruction costs no vector instruction.
+template <int EPI, int BT = 256, int NS = 2, int PRE = -1, bool SDMA = false>
 __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, uint8_t* ring,
                                            uint32_t ring_lds, uint8_t* vec, uint32_t vec_lds,
-                                           int wave, bool first = true, bool has_next = false,
-                                           int tm2 = 0, int tn2 = 0, uint32_t vec_lds2 = 0) {
-  static_assert(!PERSIST || (EPI == EPI_BIAS && BT == 256 && NS == 2 && SDMA), "persistent form");
+                                           int wave) {
   constexpr int BM = BT, BN = BT, BK = 128, WGM = 2, WGN = 2;
   constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
   constexpr int HALF = BM * BK;            // one operand of one stage (32 KB at BT = 256)
@@ -199,32 +186,38 @@ __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, 
   static_assert(DMA_A % 2 == 0, "A blocks alternate between the two swizzle parities");
 
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * (EPI == EPI_SWIGLU ? BN / 2 : BN);
-  // The lane index comes from mbcnt and the wave index arrives as a scalar, so
-  // in the persistent form no per-lane value stays live across tiles (holding
-  // the work-item id there costs a spill whose reload drains the stores).
-  int all = -1;
-  asm volatile("" : "+s"(all));  // opaque per tile: nothing below is hoisted out of a tile loop
-  const int lane = (int)__builtin_amdgcn_mbcnt_hi(all, __builtin_amdgcn_mbcnt_lo(all, 0));
+  // The lane index comes from mbcnt and the wave index arrives as a scalar.
+  const int lane = (int)__builtin_amdgcn_mbcnt_hi(-1, __builtin_amdgcn_mbcnt_lo(-1, 0));
   const int tid_v = wave * 64 + lane;
   const int wm = wave % WGM, wn = wave / WGM;
 
   const int64_t rows_a = min((int64_t)BM, p.m - m0);
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + m0 * p.lda, (uint32_t)(rows_a * p.lda));
   __amdgpu_buffer_rsrc_t rw;
+  // A tile whose A and W rows all lie inside the operands.  Only such tiles use
+  // the scalar-offset DMA: it puts the 16-row block step in soffset, which the
+  // buffer range check does not cover, so in a partial tile it would read rows
+  // past the operand's end.  Partial tiles keep every row step in the lane
+  // offset, where the range check turns rows past the end into zeros.
+  bool full = rows_a == BM;
   if constexpr (EPI == EPI_SWIGLU) {
     // Waves 0-1 load tile rows 0..BN/2-1 = value rows n0.., waves 2-3 load tile
     // rows BN/2.. = gate rows half_n + n0.. (the resource is based BN/2 rows
     // earlier, so tile row r maps to half_n + n0 + r - BN/2).
     static_assert(DMA_A * 8 * 2 == BN / 2, "each wave loads rows of one half");
     const int64_t rows_h = min((int64_t)(BN / 2), p.half_n - n0);
+    full = full && rows_h == BN / 2;
     if (wave < 2)
       rw = make_rsrc(p.w + n0 * p.ldw, (uint32_t)(rows_h * p.ldw));
     else
       rw = make_rsrc(p.w + (p.half_n + n0 - BN / 2) * p.ldw, (uint32_t)((BN / 2 + rows_h) * p.ldw));
   } else {
     const int64_t rows_w = min((int64_t)BN, p.n - n0);
+    full = full && rows_w == BN;
     rw = make_rsrc(p.w + n0 * p.ldw, (uint32_t)(rows_w * p.ldw));
   }
+  // Wave-uniform in the compiler's analysis (the tile coordinates are).
+  full = __builtin_amdgcn_readfirstlane((int)full) != 0;
 
   // DMA lane map: 1 KB block b of an operand holds rows 8b..8b+7; lane l fills
   // row 8b + l/8, slot l%8, from logical chunk (l%8) ^ lds_swizzle(row).  The
@@ -281,8 +274,8 @@ __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, 
                    d.kb + (w / 2) * w_step);
     }
   };
-  auto issue = [&](int j, int s) {
-    if constexpr (SDMA) {
+  auto issue = [&](int j, int s, auto use_sdma) {
+    if constexpr (use_sdma) {
       const SDma d = sdma_setup(j, s);
       static_for<DMA>([&](auto i) { sdma_one(d, i); });
     } else {
@@ -333,94 +326,74 @@ __device__ __forceinline__ void pipe2_tile(const GemmParams& p, int tm, int tn, 
   constexpr bool LORA_PRE = EPI == EPI_LORA && BT == 128;
   v16f lora_d[LORA_PRE ? MB * NB : 1];
   if constexpr (LORA_PRE) lora_blocks<BM, BN, WGM, WGN>(p, m0, n0, wm, wn, lane, lora_d);
-  constexpr int STORES = PERSIST ? NB * MB * 2 : 0;  // direct_epilogue's stores per wave
-  if (!PERSIST || first) {
+  // Prologue and K loop; use_sdma selects the scalar-offset DMA (full tiles).
+  auto main_loop = [&](auto use_sdma) {
     stage_vectors<BM, BN, EPI == EPI_SWIGLU>(p, m0, n0, wave, lane, vec_lds);
-    static_for<NS>([&](auto s) { issue((int)s, (int)s); });
+    static_for<NS>([&](auto s) { issue((int)s, (int)s, use_sdma); });
     wait_vmcnt<(NS - 1) * DMA, true>();
-  } else {
-    wait_vmcnt<(NS - 1) * DMA + STORES, true>();  // the previous tile's stores may drain
-  }
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-  read(I0{}, I0{});
-  // The first fragments have landed before the loop: the compiler's wait
-  // tracking then sees the same pending LDS reads on both loop entries and
-  // waits only for the fragments each MFMA needs.
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt/expcnt untouched
-  int j = 0;  // slot of stage kt
-  for (int kt = 0; kt < KT; ++kt) {
-    const int jn = j + 1 == NS ? 0 : j + 1;  // slot of stage kt + 1
-    // Substep 0 of stage kt, while reading substep 1 of the same stage.
-    mfmas(I0{}, I0{}, std::integral_constant<int, Q>{});
-    read(j, I1{});
-    interleave(std::integral_constant<int, (RD < Q ? RD : Q)>{});
-    mfmas(I1{}, I0{}, std::integral_constant<int, QB>{});
-    // The MFMAs above stay above the wait (they keep the MFMA pipe busy while
-    // the wave waits); scheduling barriers pin the order.
-    __builtin_amdgcn_sched_barrier(0);
-    // Stage kt+1 has landed for every wave (the DMAs of stages kt+2 ..
-    // kt+NS-1 may still be in flight); stage kt is fully read.
-    if (PERSIST && kt == 0 && !first)
-      wait_vmcnt<(NS - 2) * DMA + STORES, true>();
-    else
-      wait_vmcnt<(NS - 2) * DMA, true>();
-    asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    // Second half: each remaining MFMA is followed by DMA / QH of the DMA
-    // instructions of stage kt+2 and by the reads of one fragment of stage kt+1
-    // (unused after the last stage), so DMA issue and reads overlap the MFMA pipe.
-    const Dma d = dma_setup(j, kt + NS);
-    const SDma sd = sdma_setup(j, kt + NS);
-    static_for<QA>([&](auto i) {
-      constexpr int q = QB + i, nb = q / MB, mb = q % MB;
-      acc[nb][mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-          F[1][MB + nb], F[1][mb], acc[nb][mb], 0, 0, 0, 0, 0, 0);
-      static_for<DMA / QA>([&](auto t) {
-        constexpr int di = i * (DMA / QA) + t;
-        if constexpr (SDMA)
-          sdma_one(sd, std::integral_constant<int, di>{});
-        else
-          dma_one(d, std::integral_constant<int, di>{});
-      });
-      if constexpr (i < MB + NB) read_one(jn, I0{}, i);
+    read(I0{}, I0{});
+    // The first fragments have landed before the loop: the compiler's wait
+    // tracking then sees the same pending LDS reads on both loop entries and
+    // waits only for the fragments each MFMA needs.
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt/expcnt untouched
+    int j = 0;  // slot of stage kt
+    for (int kt = 0; kt < KT; ++kt) {
+      const int jn = j + 1 == NS ? 0 : j + 1;  // slot of stage kt + 1
+      // Substep 0 of stage kt, while reading substep 1 of the same stage.
+      mfmas(I0{}, I0{}, std::integral_constant<int, Q>{});
+      read(j, I1{});
+      interleave(std::integral_constant<int, (RD < Q ? RD : Q)>{});
+      mfmas(I1{}, I0{}, std::integral_constant<int, QB>{});
+      // The MFMAs above stay above the wait (they keep the MFMA pipe busy while
+      // the wave waits); scheduling barriers pin the order.
       __builtin_amdgcn_sched_barrier(0);
-    });
-    // Fragments not covered above (smaller tiles have fewer MFMAs than fragments).
-    static_for<(MB + NB > QA ? MB + NB - QA : 0)>([&](auto i) {
-      read_one(jn, I0{}, std::integral_constant<int, QA + i>{});
-    });
-    j = jn;
+      // Stage kt+1 has landed for every wave (the DMAs of stages kt+2 ..
+      // kt+NS-1 may still be in flight); stage kt is fully read.
+      wait_vmcnt<(NS - 2) * DMA, true>();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      // Second half: each remaining MFMA is followed by DMA / QH of the DMA
+      // instructions of stage kt+2 and by the reads of one fragment of stage kt+1
+      // (unused after the last stage), so DMA issue and reads overlap the MFMA pipe.
+      const Dma d = dma_setup(j, kt + NS);
+      const SDma sd = sdma_setup(j, kt + NS);
+      static_for<QA>([&](auto i) {
+        constexpr int q = QB + i, nb = q / MB, mb = q % MB;
+        acc[nb][mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+            F[1][MB + nb], F[1][mb], acc[nb][mb], 0, 0, 0, 0, 0, 0);
+        static_for<DMA / QA>([&](auto t) {
+          constexpr int di = i * (DMA / QA) + t;
+          if constexpr (use_sdma)
+            sdma_one(sd, std::integral_constant<int, di>{});
+          else
+            dma_one(d, std::integral_constant<int, di>{});
+        });
+        if constexpr (i < MB + NB) read_one(jn, I0{}, i);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      // Fragments not covered above (smaller tiles have fewer MFMAs than fragments).
+      static_for<(MB + NB > QA ? MB + NB - QA : 0)>([&](auto i) {
+        read_one(jn, I0{}, std::integral_constant<int, QA + i>{});
+      });
+      j = jn;
+    }
+  };
+  if constexpr (SDMA) {
+    if (full)
+      main_loop(std::true_type{});
+    else
+      main_loop(std::false_type{});
+  } else {
+    main_loop(std::false_type{});
   }
   wait_vmcnt<0, true>();  // every DMA has landed before the ring is reused
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  if constexpr (PERSIST) {
-    // The ring is free since the barrier above; the other vector buffer was
-    // last read by the previous tile's epilogue, before this tile's barriers.
-    if (has_next) {
-      const int64_t m2 = (int64_t)tm2 * BM, n2 = (int64_t)tn2 * BN;
-      const int64_t ra_rows = min((int64_t)BM, p.m - m2), rw_rows = min((int64_t)BN, p.n - n2);
-      const SDma d0{make_rsrc(p.a + m2 * p.lda, (uint32_t)(ra_rows * p.lda)),
-                    make_rsrc(p.w + n2 * p.ldw, (uint32_t)(rw_rows * p.ldw)), wave_lds, 0u};
-      SDma d1 = d0;
-      d1.base = wave_lds + SLOT;
-      d1.kb = BK;
-      if (KT < 2) {  // one-stage K: the second slot loads nothing
-        d1.ra = ra_none;
-        d1.rw = rw_none;
-        d1.kb = 0u;
-      }
-      stage_vectors<BM, BN, false>(p, m2, n2, wave, lane, vec_lds2);
-      static_for<DMA>([&](auto i) { sdma_one(d0, i); });
-      static_for<DMA>([&](auto i) { sdma_one(d1, i); });
-    }
-    direct_epilogue<BM, BN, WGM, WGN>(p, acc, m0, n0, wm, wn, lane, vec);
-  } else {
-    gemm_epilogue<BM, BN, WGM, WGN, EPI, true>(p, acc, m0, n0, wm, wn, tid_v, ring, vec,
-                                               LORA_PRE ? lora_d : nullptr);
-  }
+  gemm_epilogue<BM, BN, WGM, WGN, EPI, true>(p, acc, m0, n0, wm, wn, tid_v, ring, vec,
+                                             LORA_PRE ? lora_d : nullptr);
 }
 
 template <int EPI, int PRE = -1, bool SDMA = false>
@@ -451,59 +424,6 @@ __global__ void __launch_bounds__(256, NS == 2 ? 2 : 1) fp8_gemm_pipe2s(const Ge
                            __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6));
 }
 
-// Persistent 256x256 EPI_BIAS form with the direct-store epilogue: one
-// workgroup per CU walks its share of the tiles, and tile i's stores drain
-// while tile i+1's first stages load.  Workgroup b runs on XCD b % 8; XCD x
-// owns the x-th contiguous run of logical tiles (grouped order), handed
-// round-robin to the XCD's workgroups.
-template <int PRE>
-__global__ void __launch_bounds__(256) fp8_gemm_persist2(const GemmParams p) {
-  __shared__ __attribute__((aligned(1024))) uint8_t ring[PIPE2_LDS];
-  __shared__ __attribute__((aligned(1024))) uint8_t vec[2][VEC_LDS];  // alternate per tile
-  const int tiles_m = (int)((p.m + 255) / 256), tiles_n = (int)((p.n + 255) / 256);
-  const int T = tiles_m * tiles_n, G = gridDim.x, b = blockIdx.x;
-  int first, end, stride;
-  if (G >= 8 && (G & 7) == 0) {
-    const int x = b & 7, q = T >> 3, rem = T & 7;
-    first = x * q + min(x, rem) + (b >> 3);
-    end = x * q + min(x, rem) + q + (x < rem ? 1 : 0);
-    stride = G >> 3;
-  } else {
-    first = b;
-    end = T;
-    stride = G;
-  }
-  int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-  uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(ring));
-  uint32_t vec_lds = __builtin_amdgcn_readfirstlane(lds_addr(vec[0]));
-  asm volatile("" : "+s"(wave), "+s"(ring_lds), "+s"(vec_lds));
-  int tm, tn;
-  if (first < end) grouped_tile(first, tiles_m, tiles_n, p.group_m, tm, tn);
-  int cur = 0;
-  for (int logical = first; logical < end; logical += stride) {
-    const int next = logical + stride;
-    const bool has_next = next < end;
-    int tm2 = 0, tn2 = 0;
-    if (has_next) grouped_tile(next, tiles_m, tiles_n, p.group_m, tm2, tn2);
-    pipe2_tile<EPI_BIAS, 256, 2, PRE, true, true>(
-        p, tm, tn, ring, ring_lds, vec[cur], vec_lds + cur * VEC_LDS, wave, logical == first,
-        has_next, tm2, tn2, vec_lds + (1 - cur) * VEC_LDS);
-    tm = tm2;
-    tn = tn2;
-    cur = 1 - cur;
-  }
-}
-
-int compute_units();
-
-template <int PRE>
-static hipError_t launch_persist2(const GemmParams& p, hipStream_t s) {
-  const int64_t tiles = ((p.m + 255) / 256) * ((p.n + 255) / 256);
-  const int64_t grid = tiles < compute_units() ? tiles : compute_units();
-  fp8_gemm_persist2<PRE><<<dim3((unsigned)grid), dim3(256), 0, s>>>(p);
-  return hipGetLastError();
-}
-
 template <int EPI, int PRE = -1, bool SDMA = false>
 static hipError_t launch_pipe2(const GemmParams& p, hipStream_t s) {
   const int64_t tile_cols = EPI == EPI_SWIGLU ? (p.half_n + 127) / 128 : (p.n + 255) / 256;
@@ -519,10 +439,6 @@ static hipError_t launch_pipe2s(const GemmParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
-int compute_units();
-
-
-
 template <int BM, int BN, int WGM, int WGN, int EPI>
 static hipError_t launch_cfg(const GemmParams& p, hipStream_t s) {
   const int64_t tiles = ((p.m + BM - 1) / BM) * ((p.n + BN - 1) / BN);
@@ -530,66 +446,41 @@ static hipError_t launch_cfg(const GemmParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Tile configurations (BM x BN, waves M x N): 0 = automatic,
-// 1 = 256x256 (2x2), 2 = 128x128 (2x2), 3 = 64x64 (2x2; 128x128 for GELU,
-// whose row maxima need 64-column wave groups), 4 = 128x256 (2x2),
-// 5 = 256x128 (2x2), 6 = 256x256 (4x2: two waves per SIMD),
-// 7 = 256x256 (2x4: two waves per SIMD), 10 = 256x256 two-slot pipelined,
-// 128-byte stages, 12 = 128x128 two-slot pipelined (2x2 waves of 64x64, two
-// workgroups per CU),
-// 13 / 14 = 128x128 with four / three stage slots (one workgroup per CU).
-//
-// Automatic choice: the 64x64 tile below 256 tiles of 128x128, else whichever of
-// tile 17 (256x256, one workgroup per CU) and tile 12 (128x128, two per CU)
-// needs fewer rounds of tiles, a 128x128 round counting 0.5 x 1.15 of a 256x256
-// round (a quarter of the work at two per CU, at the 128x128 tile's lower
-// efficiency).  The model gives the measured ratios: 1.16 in favour of tile 17 at
-// 4096x3072x3072 (192 against 768 tiles) and 1.74 in favour of tile 12 at
-// M=1024, K=1536, N=6144 (96 against 384 tiles).
 int compute_units();
+
+// The three tilings and the rule that picks one from the shape alone:
+//   GEMM_TILE_64:  register-staged 64x64 tiles, for grids of fewer than 256
+//                  tiles of 128x128;
+//   GEMM_TILE_128: the two-slot pipeline on 128x128 tiles (2x2 waves of 64x64),
+//                  two workgroups per CU;
+//   GEMM_TILE_256: the two-slot pipeline on 256x256 tiles (2x2 waves of
+//                  128x128), barrier after K-substep 0, scalar-offset DMA in
+//                  full tiles when K % 128 == 0; one workgroup per CU.
+// Between the last two, whichever needs fewer rounds of tiles, a 128x128 round
+// counting 0.5 x 1.15 of a 256x256 round (a quarter of the work at two per CU,
+// at the 128x128 tile's lower efficiency).  The model gives the measured
+// ratios: 1.16 in favour of 256x256 at 4096x3072x3072 (192 against 768 tiles)
+// and 1.74 in favour of 128x128 at M=1024, K=1536, N=6144 (96 against 384
+// tiles).  Every tiling multiplies each output's K stages in the same order
+// with the same MFMA and shares the epilogue, so the choice never changes a
+// result bit.
+enum { GEMM_TILE_64 = 0, GEMM_TILE_128 = 1, GEMM_TILE_256 = 2 };
+
 int pick_tile(const GemmParams& p) {
   auto tiles = [&](int bm, int bn) { return ((p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn); };
   const int64_t t128 = tiles(128, 128), t256 = tiles(256, 256), cus = compute_units();
-  if (t128 < 256) return 3;
+  if (t128 < 256) return GEMM_TILE_64;
   const double rounds256 = (double)((t256 + cus - 1) / cus);
   const double rounds128 = (double)((t128 + 2 * cus - 1) / (2 * cus)) * 0.5 * 1.15;
-  return rounds256 <= rounds128 ? 17 : 12;
+  return rounds256 <= rounds128 ? GEMM_TILE_256 : GEMM_TILE_128;
 }
 
 template <int EPI>
 hipError_t launch_epi(const GemmParams& p, int tile, hipStream_t s) {
   switch (tile) {
-    case 1: return launch_cfg<256, 256, 2, 2, EPI>(p, s);
-    case 2: return launch_cfg<128, 128, 2, 2, EPI>(p, s);
-    case 3:
-      if constexpr (EPI == EPI_GELU) return launch_cfg<128, 128, 2, 2, EPI>(p, s);
-      else return launch_cfg<64, 64, 2, 2, EPI>(p, s);
-    case 4: return launch_cfg<128, 256, 2, 2, EPI>(p, s);
-    case 5: return launch_cfg<256, 128, 2, 2, EPI>(p, s);
-    case 6: return launch_cfg<256, 256, 4, 2, EPI>(p, s);
-    case 7: return launch_cfg<256, 256, 2, 4, EPI>(p, s);
-    case 10: return launch_pipe2<EPI>(p, s);
-    case 12: return launch_pipe2s<EPI, 2>(p, s);
-    case 13: return launch_pipe2s<EPI, 4>(p, s);
-    case 14: return launch_pipe2s<EPI, 3>(p, s);
-    // Schedules of tile 10: barrier after substep 0 (15), scalar-offset DMA (16),
-    // both (17, the default for large shapes).  The scalar-offset forms need
-    // K % 128 == 0 and fall back to the vector-offset DMA otherwise.
-    case 15: return launch_pipe2<EPI, 0, false>(p, s);
-    case 16: return p.k % 128 ? launch_pipe2<EPI>(p, s) : launch_pipe2<EPI, -1, true>(p, s);
-    case 17: return p.k % 128 ? launch_pipe2<EPI, 0, false>(p, s) : launch_pipe2<EPI, 0, true>(p, s);
-    // Tile 12 with tile 17's schedule.
-    case 18: return p.k % 128 ? launch_pipe2s<EPI, 2, 0, false>(p, s)
-                              : launch_pipe2s<EPI, 2, 0, true>(p, s);
-    // Tile 17's schedule as a persistent grid whose epilogue stores from
-    // registers while the next tile loads (EPI_BIAS without planes, K % 128 == 0,
-    // 16-byte output rows); other cases run tile 17.
-    case 19:
-      if constexpr (EPI == EPI_BIAS) {
-        if (p.k % 128 == 0 && p.plane_cols == 0 && p.ldo % 8 == 0 &&
-            (reinterpret_cast<uintptr_t>(p.out) & 15) == 0 && 256 * p.ldo * 2 < (int64_t(1) << 31))
-          return launch_persist2<0>(p, s);
-      }
+    case GEMM_TILE_64: return launch_cfg<64, 64, 2, 2, EPI>(p, s);
+    case GEMM_TILE_128: return launch_pipe2s<EPI, 2>(p, s);
+    case GEMM_TILE_256:
       return p.k % 128 ? launch_pipe2<EPI, 0, false>(p, s) : launch_pipe2<EPI, 0, true>(p, s);
     default: return hipErrorInvalidValue;
   }
@@ -610,13 +501,12 @@ int compute_units() {
 }
 
 hipError_t launch_fp8_gemm(const GemmParams& p, int epi, hipStream_t s) {
-  int tile = p.tile ? p.tile : pick_tile(p);
+  const int tile = pick_tile(p);
   switch (epi) {
     case EPI_BIAS: return launch_epi<EPI_BIAS>(p, tile, s);
-    case EPI_GELU: return launch_epi<EPI_GELU>(p, tile, s);
     case EPI_GATE: return launch_epi<EPI_GATE>(p, tile, s);
     case EPI_LORA: return launch_epi<EPI_LORA>(p, tile, s);
-    case EPI_SWIGLU:  // one tiling: 128 value + 128 gate columns, tile 17's schedule
+    case EPI_SWIGLU:  // one tiling: 128 value + 128 gate columns, the 256x256 schedule
       return p.k % 128 ? launch_pipe2<EPI_SWIGLU, 0, false>(p, s)
                        : launch_pipe2<EPI_SWIGLU, 0, true>(p, s);
     default: return hipErrorInvalidValue;

@@ -37,7 +37,7 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group_
 // Phase 1 (per wave, from the accumulators): a lane holds, for 32x32 block
 // (nb, mb) and register r, tile row mb*32 + (lane & 31) and tile column
 // nb*32 + 8*(r/4) + 4*(lane/32) + r%4 of its wave's sub-tile.  It applies the
-// scales, bias and the register-level epilogue (GELU, LoRA merge), rounds to
+// scales, bias and the register-level epilogue (LoRA merge), rounds to
 // bf16 and writes the values into a BM x BN bf16 staging tile in LDS (16-byte
 // chunk c of row r stored in slot c ^ (r % chunks-per-row)).  Scale and bias
 // vectors are loaded once, before any store.
@@ -147,10 +147,6 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
   const float* __restrict__ sw_p = p.sw;
   const uint16_t* __restrict__ bias_p = p.bias;
 
-  constexpr int NG = NB / 2 > 0 ? NB / 2 : 1;  // 64-column groups per wave (GELU maxima)
-  // |g| maxima per (row block, 64-column group), NaN propagated (abs_max_pk).
-  uint32_t rmax[MB][NG];
-  static_for<MB>([&](auto i) { static_for<NG>([&](auto j) { rmax[i][j] = 0u; }); });
   float sam[MB];
   static_for<MB>([&](auto mb) {
     const int row = wm * WM + mb * 32 + fr;
@@ -221,10 +217,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
                                       acc[nb][mb][g * 4 + i1] * sam[mb] * sv[g][i1]);
             if constexpr (has_bias)
               pw = pack_bf16x2(bf16_lo(pw) + bv[g][i0], bf16_hi(pw) + bv[g][i1]);
-            if constexpr (EPI == EPI_GELU) {
-              pw = pack_bf16x2(gelu_tanh(bf16_lo(pw)), gelu_tanh(bf16_hi(pw)));
-              rmax[mb][nb / 2] = abs_max_pk(rmax[mb][nb / 2], pw);
-            } else if constexpr (EPI == EPI_LORA) {
+            if constexpr (EPI == EPI_LORA) {
               uint32_t dp = pack_bf16x2(d[g * 4 + i0], d[g * 4 + i1]);
               if (p.lora_scale != 1.0f)
                 dp = pack_bf16x2(bf16_lo(dp) * p.lora_scale, bf16_hi(dp) * p.lora_scale);
@@ -246,21 +239,6 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
   else
     phase1(std::false_type{});
 
-  if constexpr (EPI == EPI_GELU) {
-    static_assert(NB % 2 == 0, "GELU epilogue needs 64-column wave groups");
-    // Lanes l and l + 32 hold the same row; each pair of 32-column blocks is
-    // one 64-column group.  One partial maximum per (row, group).
-    const int parts = (int)((p.n + 63) / 64);
-    static_for<MB>([&](auto mb) {
-      const int64_t m = m0 + wm * WM + mb * 32 + fr;
-      static_for<NB / 2>([&](auto gi) {
-        const float r = abs_max_value(rmax[mb][gi]);
-        const float v = nan_max(r, __uint_as_float((uint32_t)__shfl_xor((int)__float_as_uint(r), 32, 64)));
-        const int64_t col = n0 + wn * WN + gi * 64;
-        if (fh == 0 && m < p.m && col < p.n) p.amax_part[m * parts + col / 64] = v;
-      });
-    });
-  }
   __syncthreads();
 
   if constexpr (EPI == EPI_SWIGLU) {
@@ -276,7 +254,6 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
     const int rows = (int)min((int64_t)BM, p.m - m0);
     const int parts = (int)((p.half_n + BN / 2 - 1) / (BN / 2));
     const int part = (int)(n0 / (BN / 2));
-    const float nlog2e = -1.4426950408889634f;
 #pragma unroll 4
     for (int it = 0; it < BM / RPO; ++it) {
       const int row = r0 + it * RPO;
@@ -290,8 +267,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
       for (int j = 0; j < 4; ++j) {
         const uint32_t vw = (uint32_t)vv[j], gw = (uint32_t)gg[j];
         const float g0 = bf16_lo(gw), g1 = bf16_hi(gw);
-        const uint32_t sp = pack_bf16x2(g0 * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g0 * nlog2e)),
-                                        g1 * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g1 * nlog2e)));
+        const uint32_t sp = pack_bf16x2(silu_of_bf16(g0), silu_of_bf16(g1));
         const uint32_t hw = pack_bf16x2(bf16_lo(vw) * bf16_lo(sp), bf16_hi(vw) * bf16_hi(sp));
         amax_pk = abs_max_pk(amax_pk, hw);
         h[j] = (int)hw;

@@ -5,7 +5,7 @@
 
 namespace vfa {
 
-enum { EPI_BIAS = 0, EPI_GELU = 1, EPI_GATE = 2, EPI_LORA = 3, EPI_SWIGLU = 4 };
+enum { EPI_BIAS = 0, EPI_GATE = 2, EPI_LORA = 3, EPI_SWIGLU = 4 };
 
 struct GemmParams {
   const uint8_t* a;  // activation codes [m, k], row stride lda bytes
@@ -22,7 +22,7 @@ struct GemmParams {
   int64_t ldo;
   int64_t plane_cols;    // > 0: column n goes to plane n / plane_cols
   int64_t plane_stride;  // elements between planes
-  float* amax_part;      // EPI_GELU: [m, ceil(n / 64)] per-row maxima of |out|
+  float* amax_part;      // EPI_SWIGLU: [m, ceil(n / 256)] per-row maxima of |out|
   const uint16_t* gate;  // EPI_GATE: gate[g * gate_ts + n * gate_hs] for output row m, with
   int64_t gate_ts, gate_hs;  // g = m % gate_tokens, or gate_index[m % gate_tokens] (< gate_rows)
   int64_t gate_tokens;
@@ -38,7 +38,6 @@ struct GemmParams {
   float lora_scale, lora_strength;
   int64_t half_n;  // EPI_SWIGLU: columns [0, half_n) are values, [half_n, n) gates
   int group_m;  // tile-order group height
-  int tile;     // tile configuration (0 = automatic)
 };
 
 // RMSNorm + adaLN modulation + per-token E4M3 quantization (producer.hip).

@@ -15,13 +15,6 @@
 
 namespace vfa {
 
-__device__ __forceinline__ void pad_row(uint8_t* codes, float* scales, int64_t row, int64_t k,
-                                        int lane) {
-  uint8_t* c = codes + row * k;
-  for (int64_t j = lane; j < k; j += 64) c[j] = 0;
-  if (lane == 0) scales[row] = 1.0f;
-}
-
 // Aligned path: k % 8 == 0, ldx % 8 == 0, x 16-byte aligned, k <= 512 * VPL.
 template <int VPL>
 __global__ void __launch_bounds__(256) quant_rows_vec(const uint16_t* __restrict__ x,

@@ -6,6 +6,14 @@
 
 namespace vfa {
 
+// GEMM padding row [m, m_pad): codes 0, scale 1 (one wave).
+__device__ __forceinline__ void pad_row(uint8_t* codes, float* scales, int64_t row, int64_t k,
+                                        int lane) {
+  uint8_t* c = codes + row * k;
+  for (int64_t j = lane; j < k; j += 64) c[j] = 0;
+  if (lane == 0) scales[row] = 1.0f;
+}
+
 // max |x| over 8 bf16 values (one 16-byte vector), NaN propagated (abs_max_pk).
 __device__ __forceinline__ float absmax8(v4i v) {
   uint32_t acc = 0u;

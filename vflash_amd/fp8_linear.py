@@ -30,26 +30,26 @@ from vflash_amd.producers import QuantizedRows
 
 
 def _quantize_activation_torch(matrix):
-    """Portable torch expression of the row quantizer, with 16-row GEMM padding.
+    """The reference's portable row quantizer (h3_fp8_linear.py:18-31), as torch
+    evaluates it on the value's device, with the 16-row GEMM padding.
 
-    Same arithmetic as h3_fp8_linear.py:18-31 (and the HIP kernel): fp32 row
-    maximum, ``scale = max(amax / 448, FLT_MIN)`` (1 for a zero row), codes
-    ``e4m3(clamp(x / scale, -448, 448))``.
-
-    The divisor 448 is a device tensor, not a Python scalar: torch's GPU
-    kernels compute ``tensor / python_scalar`` as a multiplication by the
-    reciprocal, which differs from IEEE division (used by the fused kernel's
-    ``div_rn`` and by this expression on the CPU) in about half of all inputs.
+    Per row: binary32 maximum of |x|, ``scale = max(amax / 448, FLT_MIN)`` (1 for
+    a zero row), codes ``e4m3(clamp(x / scale, -448, 448))``.  ``amax / 448`` is a
+    tensor divided by a Python number: torch's GPU kernels evaluate that as a
+    product with RN(1/448), its CPU kernels as a division, so on a GPU the scale
+    can sit one binary32 ulp away from the fused quantizer's IEEE quotient
+    (vflash_quantize_rows_e4m3, like the reference's Triton kernel with div_rn).
+    This mode keeps torch's own evaluation, so it returns what the reference's
+    portable mode returns on the same device.
     """
     rows = matrix.shape[0]
     if rows % 16:
         matrix = torch.nn.functional.pad(matrix, (0, 0, 0, 16 - rows % 16))
     floats = matrix.float()
     maxima = floats.abs().amax(dim=1, keepdim=True)
-    limit = torch.full((), 448.0, dtype=torch.float32, device=floats.device)
     act_scale = torch.where(
         maxima > 0,
-        (maxima / limit).clamp_min(torch.finfo(torch.float32).tiny),
+        (maxima / 448.0).clamp_min(torch.finfo(torch.float32).tiny),
         torch.ones_like(maxima),
     )
     codes = (floats / act_scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
@@ -61,12 +61,14 @@ def w8a8_supported(value: torch.Tensor) -> bool:
 
 
 class RowFP8Execution:
-    """Own the precision choice and counters without changing process globals.
+    """One precision policy for a set of row-FP8 linears, with its call counters.
 
-    ``weight-only`` restores approximate weights for an ordinary GEMM.  ``w8a8``
-    uses BF16 input, E4M3 activations/weights and fp32 per-row scales on a
-    gfx950 device.  ``measure`` may supply asynchronous profiling scopes; this
-    class inserts no synchronization, environment changes or device selection.
+    Modes: ``weight-only`` multiplies by the weight restored from its codes and
+    row scales (an ordinary torch linear); ``w8a8`` quantizes BF16 activations
+    per token to E4M3 and runs the E4M3 GEMM on a gfx950 device, refusing any
+    other input.  ``measure(name)`` optionally wraps the activation quantization
+    and the GEMM in caller-supplied scopes (for asynchronous profiling).  Calls
+    never synchronize the device, select a device or touch process state.
     """
 
     def __init__(
@@ -141,10 +143,13 @@ class RowFP8Execution:
 
 
 class RowFP8Linear(torch.nn.Module):
-    """Meta-initialized Linear replacement; assign trusted codes and row_scale.
+    """Stands in for an ``nn.Linear`` whose weight is stored as E4M3 row codes.
 
-    The original bias is preserved.  A loader must assign all meta tensors
-    before execution, and keep the intended host/device placement.
+    ``weight`` (E4M3 ``[out, in]``) and ``row_scale`` (fp32 ``[out, 1]``) start
+    on the meta device and hold no memory until a loader assigns them (for
+    example ``load_state_dict(..., assign=True)``); the module's bias is the
+    original module's bias object itself.  The forward pass is the execution's
+    ``linear`` on those tensors, on whatever device the loader placed them.
     """
 
     def __init__(self, original: torch.nn.Linear, execution: RowFP8Execution):

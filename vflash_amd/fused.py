@@ -177,11 +177,18 @@ def fp8_ffn(
         execution.observer()
     execution.calls["w8a8"] += 2
     codes, act_scale, rows = _activation(execution, value)
-    up = kernels.fp8_gemm_swiglu if activation == "swiglu" else kernels.fp8_gemm_gelu
-    with execution.measure("linear.fp8_gemm"):
-        g, amax = up(codes, act_scale, up_weight, up_scale, rows, up_bias)
-    with execution.measure("linear.activation_quantize"):
-        h_codes, h_scale = kernels.requant_rows(g, amax)
+    if activation == "swiglu":
+        # value * silu(gate) in the up projection's epilogue, with row maxima.
+        with execution.measure("linear.fp8_gemm"):
+            g, amax = kernels.fp8_gemm_swiglu(codes, act_scale, up_weight, up_scale, rows, up_bias)
+        with execution.measure("linear.activation_quantize"):
+            h_codes, h_scale = kernels.requant_rows(g, amax)
+    else:
+        # The up projection, then GELU-tanh fused with the down linear's quantization.
+        with execution.measure("linear.fp8_gemm"):
+            y = kernels.fp8_gemm(codes, act_scale, up_weight, up_scale, rows, up_bias)
+        with execution.measure("linear.activation_quantize"):
+            h_codes, h_scale, _ = kernels.gelu_quantize_rows(y)
     with execution.measure("linear.fp8_gemm"):
         out = kernels.fp8_gemm_gate_residual(
             h_codes, h_scale, down_weight, down_scale, rows, gate, res, down_bias,

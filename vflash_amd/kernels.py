@@ -146,22 +146,23 @@ def fp8_gemm_planes(codes, act_scale, weight, w_scale, rows, planes, bias=None):
     return out
 
 
-def row_parts(n: int) -> int:
-    return int(_lib.library().vflash_row_parts(n))
-
-
-def fp8_gemm_gelu(codes, act_scale, weight, w_scale, rows, bias=None):
-    """g = bf16(gelu_tanh(linear)), plus per-row |g| maxima per 64-column group."""
-    device = _gemm_operands(codes, act_scale, weight, w_scale, rows, bias)
-    n, k = weight.shape
-    g = torch.empty((rows, n), device=device, dtype=torch.bfloat16)
-    parts = row_parts(n)
-    amax = torch.empty((rows, parts), device=device, dtype=torch.float32)
-    if rows:
-        call("vflash_fp8_linear_gelu", ptr(codes), ptr(act_scale), codes.stride(0), ptr(weight),
-             ptr(w_scale), weight.stride(0), rows, n, k, ptr(bias), ptr(g), g.stride(0),
-             ptr(amax), stream_of(device))
-    return g, amax
+def gelu_quantize_rows(y, pad_to: int = 16, keep_values: bool = False):
+    """E4M3 codes [ceil16(M), K] and fp32 scales [ceil16(M), 1] of g = bf16(gelu_tanh(y)),
+    and g itself (bf16 [M, K]) with ``keep_values`` (else None)."""
+    if y.dtype != torch.bfloat16 or y.ndim != 2 or y.stride(1) != 1:
+        raise ValueError("the GELU quantizer requires a 2-D BF16 matrix with unit column stride")
+    m, k = y.shape
+    if k % 8 or k > 16384 or y.stride(0) % 8 or y.data_ptr() % 16:
+        raise ValueError("the GELU quantizer needs K % 8 == 0, K <= 16384 and 16-byte aligned rows")
+    device = require_device(y)
+    m_pad = (m + pad_to - 1) // pad_to * pad_to
+    codes = torch.empty((m_pad, k), device=device, dtype=E4M3)
+    scales = torch.empty((m_pad, 1), device=device, dtype=torch.float32)
+    g = torch.empty((m, k), device=device, dtype=torch.bfloat16) if keep_values else None
+    if m:
+        call("vflash_gelu_quantize_rows_e4m3", ptr(y), m, k, y.stride(0), ptr(g), k, ptr(codes),
+             ptr(scales), m_pad, stream_of(device))
+    return codes, scales, g
 
 
 def swiglu_parts(n: int) -> int:
@@ -321,12 +322,22 @@ def nvfp4_gemm(codes, act_scale, packed, block_scales, alpha, rows, bias=None):
         raise ValueError("NVFP4 activation codes must be a 2-D float8_e4m3fn matrix")
     if packed.dtype != torch.uint8 or block_scales.dtype != torch.uint8:
         raise ValueError("NVFP4 weights and block scales must be uint8")
+    if packed.ndim != 2 or not packed.is_contiguous():
+        raise ValueError("NVFP4 packed weights must be a contiguous uint8 [N, K/2] matrix")
     n, half_k = packed.shape
     k = 2 * half_k
-    if codes.shape[1] != k:
+    if codes.shape[1] != k or codes.shape[0] < rows:
         raise ValueError("NVFP4 activation width differs from the weight")
+    if block_scales.shape != (n, k // 16) or not block_scales.is_contiguous():
+        raise ValueError("NVFP4 block scales must be a contiguous uint8 [N, K/16] matrix")
+    if act_scale.dtype != torch.float32 or not act_scale.is_contiguous() or act_scale.numel() < rows:
+        raise ValueError("NVFP4 activation scales must be contiguous fp32 covering the rows")
     if alpha.dtype != torch.float32 or alpha.numel() != 1:
         raise ValueError("NVFP4 alpha must be an fp32 scalar tensor")
+    if bias is not None and (bias.dtype != torch.bfloat16 or bias.shape != (n,) or not bias.is_contiguous()):
+        raise ValueError("NVFP4 bias must be a contiguous BF16 vector of the output width")
+    if block_scales.data_ptr() % 16:
+        block_scales = block_scales.clone()  # the kernel copies scale runs with 16-byte DMA
     device = require_device(codes, act_scale, packed, block_scales, alpha,
                             *([bias] if bias is not None else []))
     out = torch.empty((rows, n), device=device, dtype=torch.bfloat16)
