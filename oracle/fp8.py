@@ -16,7 +16,7 @@ from oracle.formats import FLT_MIN, bf16_round, e4m3_decode, e4m3_encode
 F32 = np.float32
 
 
-def quantize_rows(x, pad: int = 16):
+def quantize_rows(x, pad: int = 16, scalar_product: bool = False):
     """Per-token E4M3 codes and scales with GEMM row padding.
 
     Follows src/vflash/native/h3_fp8_linear.py:18-31 (and the fused kernel
@@ -24,15 +24,20 @@ def quantize_rows(x, pad: int = 16):
     scale = max(amax / 448, FLT_MIN) if amax > 0 else 1 (IEEE binary32
     division); codes = e4m3(clamp(x / scale, -448, 448)); rows padded to a
     multiple of ``pad`` with codes 0 and scale 1.
+    ``scalar_product`` forms amax / 448 as amax * RN(1/448) instead: how torch's
+    GPU kernels evaluate the reference's portable expression ``maxima / 448.0``
+    (a tensor divided by a Python number); its CPU kernels divide.
     Pinned by: the reference KATs (tests/test_fp8_linear.py:99-120, restated in
-    tests/golden), torch's float8_e4m3fn cast, and closed-form invariants.
+    tests/golden), torch's float8_e4m3fn cast, and closed-form invariants; the
+    product form by torch on the GPU (tests/test_gpu_quant.py).
     """
     x = np.asarray(x, dtype=F32)
     m, k = x.shape
     m_pad = -(-m // pad) * pad if pad > 1 else m
     amax = np.max(np.abs(x), axis=1) if k else np.zeros(m, F32)
-    with np.errstate(invalid="ignore", divide="ignore"):
-        scale = np.where(amax > 0, np.maximum(amax / F32(448.0), FLT_MIN), F32(1.0)).astype(F32)
+    with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
+        base = amax * (F32(1.0) / F32(448.0)) if scalar_product else amax / F32(448.0)
+        scale = np.where(amax > 0, np.maximum(base.astype(F32), FLT_MIN), F32(1.0)).astype(F32)
         q = np.clip(x / scale[:, None], F32(-448.0), F32(448.0))
     codes = np.zeros((m_pad, k), dtype=np.uint8)
     codes[:m] = e4m3_encode(q)
@@ -68,9 +73,10 @@ def add_bias(y, bias) -> np.ndarray:
     return bf16_round(np.asarray(y, F32) + np.asarray(bias, F32).reshape(1, -1))
 
 
-def w8a8_linear(x, w_codes, sw, bias=None):
-    """RowFP8Execution.linear in w8a8 mode (h3_fp8_linear.py:98-121) for a 2-D input."""
-    codes, sa = quantize_rows(x)
+def w8a8_linear(x, w_codes, sw, bias=None, scalar_product: bool = False):
+    """RowFP8Execution.linear in w8a8 mode (h3_fp8_linear.py:98-121) for a 2-D input;
+    ``scalar_product`` selects the portable quantizer as torch evaluates it on a GPU."""
+    codes, sa = quantize_rows(x, scalar_product=scalar_product)
     m = np.asarray(x).shape[0]
     return add_bias(scaled_mm(codes[:m], sa[:m], w_codes, sw), bias)
 
