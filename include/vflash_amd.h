@@ -25,6 +25,10 @@ extern "C" {
 #define VFLASH_OK 0
 #define VFLASH_EINVAL (-1)  /* an argument is outside the declared contract */
 #define VFLASH_ELAUNCH (-2) /* the HIP runtime refused the launch */
+#define VFLASH_ESCRATCH (-3) /* the call needs more than the allocation-free entry's scratch */
+
+/* Bytes of the static device scratch of vflash_fp8_linear_swiglu_quantize_noalloc. */
+#define VFLASH_NOALLOC_SCRATCH_BYTES (16 << 20)
 
 /* Version of this interface; bumped when a signature changes. */
 int vflash_abi_version(void);
@@ -121,6 +125,28 @@ int vflash_fp8_linear_swiglu(const void* a, const float* sa, int64_t lda, const 
 
 /* Number of 128-column groups per row in the SwiGLU amax_part: ceil(n / 2 / 128). */
 int64_t vflash_swiglu_parts(int64_t n);
+
+/*
+ * vflash_fp8_linear_swiglu followed by vflash_requant_rows_e4m3 in one call
+ * that allocates nothing.  It has no counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops that forbid allocation).  The per-row partial maxima that
+ * vflash_fp8_linear_swiglu returns in amax_part stay in a static device array
+ * of VFLASH_NOALLOC_SCRATCH_BYTES (16 MiB) that each GPU the library runs on
+ * holds until the process ends; the caller passes only inputs and outputs.
+ *   h       bf16 [m, n/2] (ldh): h of vflash_fp8_linear_swiglu
+ *   codes   e4m3 [m_pad, n/2] contiguous, scales fp32 [m_pad]: the requantized h
+ *           (vflash_requant_rows_e4m3 on h), rows m..m_pad-1 codes 0, scale 1
+ *   Requires the contracts of both entries and m * vflash_swiglu_parts(n) <=
+ *   VFLASH_NOALLOC_SCRATCH_BYTES / 4; larger calls return VFLASH_ESCRATCH before
+ *   any launch.  Calls that overlap on one GPU share the array and race; a
+ *   caller serializes them (one stream per GPU, or its own ordering).
+ */
+int vflash_fp8_linear_swiglu_quantize_noalloc(const void* a, const float* sa, int64_t lda,
+                                              const void* w, const float* sw, int64_t ldw,
+                                              int64_t m, int64_t n, int64_t k, const void* bias,
+                                              void* h, int64_t ldh, void* codes, float* scales,
+                                              int64_t m_pad, void* stream);
 
 /*
  * RMSNorm + adaLN modulation fused with the consuming linear's per-token E4M3

@@ -100,3 +100,16 @@ def test_no_process_wide_tuning_state_is_exported():
     # change it for later calls.
     lib = _lib.library()
     assert not hasattr(lib, "vflash_set_gemm_tile")
+
+
+def test_noalloc_entry_refuses_oversize_calls_before_touching_a_device():
+    # m * swiglu_parts(n) beyond 16 MiB of fp32 maxima: VFLASH_ESCRATCH, no launch
+    # (the check precedes the device's scratch address lookup, so it runs here).
+    lib = _lib.library()
+    p = ctypes.c_void_p(256)
+    args = [p, p, 1024, p, p, 1024, 4194305, 256, 1024, None, p, 128, p, p, 4194320, None]
+    assert lib.vflash_fp8_linear_swiglu_quantize_noalloc(*args) == _lib.VFLASH_ESCRATCH
+    args[6], args[14] = 16, 16
+    args[7] = 200  # n % 256: outside the contract
+    assert lib.vflash_fp8_linear_swiglu_quantize_noalloc(*args) == _lib.VFLASH_EINVAL
+    assert lib.vflash_status_string(_lib.VFLASH_ESCRATCH).startswith(b"the call needs more")

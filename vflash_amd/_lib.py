@@ -18,6 +18,8 @@ LIBRARY = Path(__file__).resolve().with_name("libvflash_amd.so")
 VFLASH_OK = 0
 VFLASH_EINVAL = -1
 VFLASH_ELAUNCH = -2
+VFLASH_ESCRATCH = -3
+NOALLOC_SCRATCH_BYTES = 16 << 20
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -40,6 +42,10 @@ SIGNATURES: dict[str, tuple[list, object]] = {
         _I32,
     ),
     "vflash_swiglu_parts": ([_I64], _I64),
+    "vflash_fp8_linear_swiglu_quantize_noalloc": (
+        [_P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _I64, _P],
+        _I32,
+    ),
     "vflash_rmsnorm_modulate_quantize_e4m3": (
         [_P, _I64, _I64, _I64, _P, _F32, _P, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _P,
          _I64, _P],
@@ -96,7 +102,7 @@ def call(name: str, *args) -> None:
     if status == VFLASH_OK:
         return
     text = library().vflash_status_string(status).decode()
-    if status == VFLASH_EINVAL:
+    if status in (VFLASH_EINVAL, VFLASH_ESCRATCH):
         raise ValueError(f"{name}: {text}")
     raise KernelError(f"{name}: {text}")
 

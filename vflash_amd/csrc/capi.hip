@@ -92,6 +92,7 @@ const char* vflash_status_string(int s) {
     case VFLASH_OK: return "ok";
     case VFLASH_EINVAL: return "argument outside the declared contract";
     case VFLASH_ELAUNCH: return "HIP launch failed";
+    case VFLASH_ESCRATCH: return "the call needs more than the allocation-free entry's static scratch";
     default: return "unknown status";
   }
 }

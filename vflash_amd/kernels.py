@@ -186,6 +186,32 @@ def fp8_gemm_swiglu(codes, act_scale, weight, w_scale, rows, bias=None):
     return h, amax
 
 
+def fp8_gemm_swiglu_quantize_noalloc(codes, act_scale, weight, w_scale, rows, bias, h, h_codes,
+                                     h_scales):
+    """fp8_gemm_swiglu + requant_rows in one C-ABI call that allocates nothing: the
+    per-row partial maxima stay in the library's static device scratch.  The
+    outputs are the caller's: ``h`` bf16 [rows, F], ``h_codes`` E4M3 [ceil16(rows), F]
+    and ``h_scales`` fp32 [ceil16(rows), 1]; this wrapper allocates nothing either.
+    Calls that overlap on one GPU share the scratch and must be serialized."""
+    device = _gemm_operands(codes, act_scale, weight, w_scale, rows, bias)
+    n, k = weight.shape
+    f = n // 2
+    m_pad = h_codes.shape[0]
+    if n % 256 or h.dtype != torch.bfloat16 or h.shape != (rows, f) or h.stride(1) != 1:
+        raise ValueError("SwiGLU output must be BF16 [rows, F] with F a multiple of 128")
+    if h_codes.dtype != E4M3 or h_codes.shape[1] != f or not h_codes.is_contiguous() or m_pad < rows:
+        raise ValueError("requantized codes must be a contiguous E4M3 [>= rows, F] matrix")
+    if (h_scales.dtype != torch.float32 or h_scales.numel() != m_pad
+            or not h_scales.is_contiguous()):
+        raise ValueError("requantization scales must be contiguous fp32, one per code row")
+    require_device(h, h_codes, h_scales)
+    if rows:
+        call("vflash_fp8_linear_swiglu_quantize_noalloc", ptr(codes), ptr(act_scale), codes.stride(0),
+             ptr(weight), ptr(w_scale), weight.stride(0), rows, n, k, ptr(bias), ptr(h), h.stride(0),
+             ptr(h_codes), ptr(h_scales), m_pad, stream_of(device))
+    return h, h_codes, h_scales
+
+
 def requant_rows(g, amax_part, pad_to: int = 16):
     """E4M3 codes/scales of ``g`` using its epilogue row maxima."""
     if g.dtype != torch.bfloat16 or g.ndim != 2 or g.stride(1) != 1:
