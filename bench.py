@@ -53,6 +53,10 @@ def parse():
     )
     p.add_argument("--skinny-m", type=int, default=1024)
     p.add_argument("--skinny-n", type=int, default=6144)
+    p.add_argument("--skinny-k", type=int, default=1536,
+                   help="skinny K: 1536 (the skinny configuration) or 5376 (the audio pass's Q/K/V)")
+    p.add_argument("--skinny-rank", type=int, default=32,
+                   help="adapter rank of the skinny step (32; 128 and 16 for the shipped adapters)")
     p.add_argument("--operand-sets", type=int, default=0,
                    help="rotating operand sets for the small shapes (0 = enough to exceed the last-level cache)")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -408,7 +412,7 @@ def make_workload(args, dev):
             cpu=cpu)
 
     if wl == "skinny":
-        m, k, n, r = args.skinny_m, 1536, args.skinny_n, 32
+        m, k, n, r = args.skinny_m, args.skinny_k, args.skinny_n, args.skinny_rank
         per_set = m * k * 3 + n * k + 2 * m * n + 2 * r * (k + n) + 2 * m * r
         count = args.operand_sets or max(2, int(600e6 // per_set) + 1)  # > 2x the last-level cache
         sets = []
@@ -461,7 +465,7 @@ def make_workload(args, dev):
             return (time.perf_counter() - t0) * 1e3 / args.steps
 
         wlo = Workload(
-            wl, f"Skinny-M FP8 linear + rank-32 LoRA GB/s (M={m},K={k},N={n})", "GB/s", step_bytes, step,
+            wl, f"Skinny-M FP8 linear + rank-{r} LoRA GB/s (M={m},K={k},N={n})", "GB/s", step_bytes, step,
             "fp8_gemm_lora", gemm_bytes, "hbm", HBM_PEAK_GBS,
             {"workload": f"skinny_lora_m{m}_k{k}_n{n}_r{r}", "m": m, "k": k, "n": n, "rank": r,
              "operand_sets": count, "flops_per_step": 2.0 * m * n * k + 2.0 * m * r * (k + n)},

@@ -1,6 +1,7 @@
-"""Model of the pipelined GEMM's DMA lane map (csrc/fp8_gemm.hip, pipe2_tile).
+"""Model of the pipelined GEMM's DMA lane map (csrc/fp8_gemm_pipe.h, pipe_tile).
 
-One stage copies BT rows x 128 bytes of an operand with BT/32 buffer_load ... lds
+One stage copies BT rows x 128 bytes of an operand (BT = BM activation rows or
+BN weight rows: 64, 128, 192 or 256) with BT/32 buffer_load ... lds
 instructions per wave (4 waves).  Lane l of wave w reads row
 ``w * BT/4 + l // 8 + 8 * (i % 2) + 16 * (i // 2)`` for instruction i, chunk
 ``(l % 8) ^ swizzle``.  The buffer range check sees only the lane offset:
@@ -30,7 +31,7 @@ def uses_scalar_offset(rows_valid, bt):
     return rows_valid == bt
 
 
-@pytest.mark.parametrize("bt", [128, 256])
+@pytest.mark.parametrize("bt", [64, 128, 192, 256])
 def test_every_tile_row_is_loaded_once_per_stage(bt):
     read, _ = lane_rows(bt)
     rows = np.sort(read.reshape(-1, read.shape[-1]), axis=None)
@@ -38,8 +39,9 @@ def test_every_tile_row_is_loaded_once_per_stage(bt):
     assert np.array_equal(np.bincount(rows, minlength=bt), np.full(bt, 8))
 
 
-@pytest.mark.parametrize("bt", [128, 256])
-@pytest.mark.parametrize("rows_valid", [1, 4, 16, 17, 48, 100, 127, 128, 200, 255, 256])
+@pytest.mark.parametrize("bt", [64, 128, 192, 256])
+@pytest.mark.parametrize("rows_valid", [1, 4, 16, 17, 48, 63, 64, 100, 127, 128, 191, 192, 200,
+                                        255, 256])
 def test_no_read_past_the_operand(bt, rows_valid):
     if rows_valid > bt:
         pytest.skip("tile smaller than the valid rows")

@@ -260,10 +260,39 @@ def test_lora_linear_skinny_shapes(dev, m, n, scaling, strength):
     assert torch.equal(off, ex.linear(d(x), d(c), d(s), d(b)))
 
 
-# One shape per GEMM tiling: 64x64 (few tiles), 128x128 (the adapter products
-# ahead of the K loop), 256x256 (the adapter products in the epilogue).
+@pytest.mark.parametrize("m", [256, 1024])
+@pytest.mark.parametrize("r,scaling,strength", [(128, 1.0, 1.0), (16, 0.5, 1.375)])
+def test_lora_linear_audio_projection_shapes(dev, m, r, scaling, strength):
+    # The audio pass's separate Q/K/V projections: hidden 5376 -> inner 7168 on
+    # the live rows, with the shipped adapters' ranks (128 and 16).
+    k, n = 5376, 7168
+    g = torch.Generator().manual_seed(m * 3 + r)
+    x = torch.randn((m, k), generator=g).to(torch.bfloat16)
+    c, s = quantize_weight_rows(torch.randn((n, k), generator=g) * 0.02)
+    b = (torch.randn(n, generator=g) * 0.01).to(torch.bfloat16)
+    la = (torch.randn((r, k), generator=g) * 0.01).to(torch.bfloat16)
+    lb = (torch.randn((n, r), generator=g) * 0.01).to(torch.bfloat16)
+    d = lambda t: t.to(dev)
+    ex = RowFP8Execution("w8a8", activation_quantizer="hip")
+    out = fp8_linear_lora(ex, d(x), d(c), d(s), d(b), d(la), d(lb), scaling=scaling, strength=strength)
+    xf = x.float().numpy()
+    t = kernels.lora_down(d(x), d(la)).float().cpu().numpy()
+    rel_check(t, O.lora_delta(xf, la.float().numpy(), np.eye(r, dtype=np.float32)))
+    base = O.w8a8_linear(xf, u8(c), s.reshape(-1).numpy(), b.float().numpy())
+    delta = O.lora_delta(xf, la.float().numpy(), lb.float().numpy(), scaling, strength)
+    rel_check(out.float().cpu().numpy(), O.lora_merge(base, delta))
+    # The base linear alone, as the hook sees it before the delta.
+    base_dev = ex.linear(d(x), d(c), d(s), d(b)).float().cpu().numpy()
+    rel_check(base_dev, base)
+
+
+# Tilings with at most four 32x32 blocks per wave compute the adapter products
+# ahead of the K loop (64x64: 300 x 640, 128x64: 300 x 4112, 128x128:
+# 2100 x 7184), the others in the epilogue (128x192: 1024 x 6144, 256x192:
+# 4096 x 3072, 256x256: 4100 x 3088).
 @pytest.mark.parametrize("r", [32, 48, 128])
-@pytest.mark.parametrize("m,n,k", [(300, 640, 512), (1024, 6144, 1536), (4096, 3072, 1536)])
+@pytest.mark.parametrize("m,n,k", [(300, 640, 512), (300, 4112, 512), (2100, 7184, 384),
+                                   (1024, 6144, 1536), (4096, 3072, 1536), (4100, 3088, 256)])
 def test_lora_epilogue_under_each_tiling(dev, m, n, k, r):
     g = torch.Generator().manual_seed(m + n + k + r)
     x = torch.randn((m, k), generator=g).to(torch.bfloat16)

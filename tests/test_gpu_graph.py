@@ -62,7 +62,7 @@ def test_skinny_lora_linear_replays_from_a_graph(dev):
 
 @pytest.mark.parametrize("m,k,n", [(4096, 1024, 2048), (2100, 640, 2064)])
 def test_w8a8_linear_replays_from_a_graph(dev, m, k, n):
-    # 512 256x256 tiles (the pipelined 256x256 kernel) and a 128x128-tile shape.
+    # 256 tiles of 256x128 and 187 tiles of 128x192 (partial last tiles).
     g = torch.Generator().manual_seed(m)
     c, s = quantize_weight_rows(torch.randn((n, k), generator=g) * 0.02)
     b = (torch.randn(n, generator=g) * 0.01).to(torch.bfloat16)

@@ -14,23 +14,48 @@ pytestmark = pytest.mark.gpu
 
 
 
+# The tilings of csrc/fp8_gemm.hip (kTilings): tile rows, tile columns,
+# relative throughput per output, and whether the tiling only runs where the
+# grid fits one round.
+TILINGS = {
+    "256x256": (256, 256, 1.00, False),
+    "256x192": (256, 192, 0.95, False),
+    "256x128": (256, 128, 0.90, False),
+    "128x192": (128, 192, 0.85, False),
+    "128x128": (128, 128, 0.80, False),
+    "128x128 one round": (128, 128, 0.85, True),
+    "128x64": (128, 64, 0.60, False),
+    "64x64": (64, 64, 0.50, False),
+}
+
+
 def tiling(m, n, cus=256):
     """The GEMM tiling the library picks for an M x N output on `cus` compute
-    units (csrc/fp8_gemm.hip, pick_tile): 64 below 256 tiles of 128x128, else
-    256 or 128, whichever needs fewer rounds (a 128x128 round weighted 0.575)."""
-    t128 = -(-m // 128) * -(-n // 128)
-    t256 = -(-m // 256) * -(-n // 256)
-    if t128 < 256:
-        return 64
-    return 256 if -(-t256 // cus) <= -(-t128 // (2 * cus)) * 0.575 else 128
+    units (csrc/fp8_gemm.hip, pick_tiling): the least ceil(tiles / CUs) x tile
+    outputs / throughput, the larger tile first on ties."""
+    best = None
+    for name, (bm, bn, rate, one_round) in TILINGS.items():
+        tiles = -(-m // bm) * -(-n // bn)
+        if one_round and tiles > cus:
+            continue
+        cost = -(-tiles // cus) * bm * bn / rate
+        if best is None or cost < best[0]:
+            best = (cost, name)
+    return best[1]
 
 
-# Edge shapes under each of the three tilings: partial row and column tiles,
-# K tails (K % 128 != 0 takes the vector-offset DMA everywhere), one K stage.
+# Edge shapes under each tiling: partial row and column tiles, K tails
+# (K % 128 != 0 takes the vector-offset DMA everywhere), one K stage.
 EDGES = [
-    (1, 16, 16, 64), (17, 48, 272, 64), (300, 144, 48, 64), (257, 256, 528, 64),
-    (1040, 144, 6160, 128), (1040, 48, 6160, 128), (1100, 256, 6032, 128),
-    (4100, 144, 3088, 256), (4100, 256, 3088, 256), (4097, 128, 3072, 256),
+    (1, 16, 16, "64x64"), (17, 48, 272, "64x64"), (300, 144, 48, "64x64"),
+    (257, 256, 528, "64x64"),
+    (257, 144, 4112, "128x64"), (300, 256, 4112, "128x64"),
+    (520, 144, 4112, "128x128 one round"), (300, 256, 7184, "128x128 one round"),
+    (1040, 144, 13840, "128x128"), (2100, 256, 7184, "128x128"),
+    (257, 144, 13840, "128x192"), (700, 256, 6032, "128x192"),
+    (1040, 48, 6160, "256x128"), (1100, 256, 6032, "256x128"),
+    (1040, 144, 7184, "256x192"), (1100, 256, 8208, "256x192"),
+    (4100, 144, 3088, "256x256"), (4100, 256, 3088, "256x256"), (4097, 128, 3072, "256x256"),
 ]
 
 

@@ -41,12 +41,16 @@ def inputs(m, k, n, seed=0):
     return x, w, s, b
 
 
-# 4096 x 3088 runs 208 tiles of 256x256 (one round over 256 CUs) rather than 800
-# of 128x128 (two rounds at two per CU), so the 256x256 tiling with the
-# scalar-offset DMA (K % 128 == 0) is chosen; its last column of tiles holds
-# only 16 weight rows.  M = 4100 adds a last row of tiles with 4 activation
-# rows.  1040 x 6160 runs the 128x128 tiling with partial tiles on both edges.
-@pytest.mark.parametrize("m,n", [(4096, 3088), (4100, 3088), (4100, 3072), (1040, 6160)])
+# One shape per GEMM tiling (csrc/fp8_gemm.hip, pick_tiling), each with a
+# partial last row and column of tiles; K = 384 is a multiple of 128, so full
+# tiles take the scalar-offset DMA and partial ones the vector-offset form.
+#   4096 x 3088, 4100 x 3088, 4100 x 3072: 256x256 (16 or 4 weight rows, 4
+#   activation rows in the last tiles); 1100 x 8208: 256x192; 1040 x 6160:
+#   256x128; 700 x 6032: 128x192; 2100 x 7184: 128x128, two per CU;
+#   520 x 4112: 128x128 in one round; 300 x 4112: 128x64; 257 x 528: 64x64.
+@pytest.mark.parametrize("m,n", [(4096, 3088), (4100, 3088), (4100, 3072), (1100, 8208),
+                                 (1040, 6160), (700, 6032), (2100, 7184), (520, 4112),
+                                 (300, 4112), (257, 528)])
 def test_linear_tail_tiles_match_untailed_operands(dev, m, n):
     k = 384
     x, w, s, b = inputs(m, k, n, seed=1)

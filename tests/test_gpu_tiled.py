@@ -7,8 +7,8 @@ token matrix, on 1024-row tiles plus a 17-row remainder, and on 16384-row tiles,
 and the three results must be identical.  The widths are the configuration
 widths (hidden 5120, merged QKV 15360, FFN 13824, adapter K 1536 / N 6144), so
 the automatic GEMM tiling changes with the tile height: 256x256 on the whole
-matrix, 128x128 for 1024-row tiles of the 5120- and 6144-wide projections, and
-the register-staged 64x64 form for the 17-row remainder.
+matrix and on 16384-row tiles, 128x192 for 1024-row tiles of the 5120- and
+6144-wide projections, and 64x64 for the 17-row remainder.
 """
 
 import pytest

@@ -35,9 +35,8 @@ hipError_t launch_nvfp4(const uint8_t*, const float*, int64_t, const uint8_t*, c
 
 namespace {
 
-// Tile-order group heights: 2 for the E4M3 GEMMs and 8 for the E2M1-weight
-// GEMMs, the fastest of a sweep over 1..32 at the large shapes.
-constexpr int FP8_GROUP_M = 2;
+// Tile-order group height of the E2M1-weight GEMMs, the fastest of a sweep over
+// 1..32 at the large shapes.  The E4M3 launcher sets its own from the tiling.
 constexpr int FP4_GROUP_M = 8;
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
@@ -77,7 +76,6 @@ vfa::GemmParams base_params(const void* a, const float* sa, int64_t lda, const v
   p.ldo = ldo;
   p.lora_scale = 1.0f;
   p.lora_strength = 1.0f;
-  p.group_m = FP8_GROUP_M;
   return p;
 }
 

@@ -141,6 +141,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
   constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
   constexpr int NT = 64 * WGM * WGN;
   constexpr int CH = BN / 8;  // 16-byte chunks per staged row
+  // Chunk c of staged row r sits in slot c ^ (r % SWZ): every slot of a row
+  // when CH is a power of two, else within its aligned group of 8 (CH = 24).
+  constexpr int SWZ = (CH & (CH - 1)) == 0 ? CH : 8;
+  static_assert(CH % SWZ == 0, "swizzle stays inside the row");
   constexpr int PITCH = BN * 2;
   const int lane = tid & 63, fr = lane & 31, fh = lane >> 5;
   const float* __restrict__ sa_p = p.sa;
@@ -228,7 +232,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
             w[h] = pw;
           });
           const int c = (wn * WN + nb * 32 + g * 8) / 8;  // 16-byte chunk of the row
-          *reinterpret_cast<uint2*>(stage + row * PITCH + ((c ^ (row % CH)) << 4) + fh * 8) =
+          *reinterpret_cast<uint2*>(stage + row * PITCH + ((c ^ (row % SWZ)) << 4) + fh * 8) =
               make_uint2(w[0], w[1]);
         });
       });
@@ -258,7 +262,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
     for (int it = 0; it < BM / RPO; ++it) {
       const int row = r0 + it * RPO;
       const bool valid = row < rows;
-      const int rs = row % CH;
+      const int rs = row % SWZ;
       const v4i vv = *reinterpret_cast<const v4i*>(stage + row * PITCH + ((c ^ rs) << 4));
       const v4i gg = *reinterpret_cast<const v4i*>(stage + row * PITCH + (((c + CHO) ^ rs) << 4));
       v4i h;
@@ -288,9 +292,12 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
 
   // Phase 2: LDS rows -> global.  Thread tid owns the 16-byte column chunk
   // c = tid % CH of rows tid / CH + RPP * it, so its column, plane and
-  // bounds are computed once.
+  // bounds are computed once.  When CH does not divide the thread count
+  // (CH = 24), the last NT - RPP * CH threads have no chunk.
   constexpr int RPP = NT / CH;  // rows per pass
-  static_assert(NT % CH == 0 && BM % RPP == 0, "whole phase-2 passes");
+  constexpr int PASSES = (BM + RPP - 1) / RPP;
+  static_assert(RPP >= 1, "one row per pass at least");
+  if (tid >= RPP * CH) return;
   const int c = tid % CH, r0 = tid / CH;
   const int64_t n = n0 + c * 8;
   if (n >= p.n) return;
@@ -302,11 +309,11 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
   }
   auto pass = [&](auto vec_out) {
 #pragma unroll 8
-    for (int it = 0; it < BM / RPP; ++it) {
+    for (int it = 0; it < PASSES; ++it) {
       const int row = r0 + it * RPP;
       if (row >= rows) break;
       const int64_t m = m0 + row;
-      v4i v = *reinterpret_cast<const v4i*>(stage + row * PITCH + ((c ^ (row % CH)) << 4));
+      v4i v = *reinterpret_cast<const v4i*>(stage + row * PITCH + ((c ^ (row % SWZ)) << 4));
       if constexpr (EPI == EPI_GATE) {
         const uint16_t* res = p.residual + m * p.ldr + n;
         // Gate row of output row m: token m % gate_tokens, through the index when
@@ -346,75 +353,6 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
     pass(std::true_type{});
   else
     pass(std::false_type{});
-}
-
-// Epilogue of EPI_BIAS tiles without LDS staging: the scale/bias arithmetic of
-// gemm_epilogue's phase 1, then global stores straight from the accumulator
-// layout.  In a 32x32 block lane l holds row l % 32 and, per group g of four
-// registers, columns 8g + 4(l / 32) .. +3; v_permlane32_swap exchanges groups
-// between the lane halves so that a lane holds 8 consecutive columns of its
-// row (lanes 0-31 columns 16q .. +7, lanes 32-63 columns 16q + 8 .. +15) and
-// writes them with one 16-byte buffer store.  Stores outside the matrix are
-// dropped: rows past the end by the resource range, columns past the end by a
-// killed offset.  The ring is not touched, so the next tile's DMA may start
-// while these stores drain.  Requires ldo % 8 == 0, out 16-byte aligned,
-// 256 * ldo * 2 < 2^31.
-template <int BM, int BN, int WGM, int WGN>
-__device__ __forceinline__ void direct_epilogue(const GemmParams& p,
-                                                v16f (&acc)[BN / WGN / 32][BM / WGM / 32],
-                                                int64_t m0, int64_t n0, int wm, int wn, int lane,
-                                                const uint8_t* vec) {
-  constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
-  const int fr = lane & 31, fh = lane >> 5;
-  const int64_t rows = min((int64_t)BM, p.m - m0), cols = min((int64_t)BN, p.n - n0);
-  const __amdgpu_buffer_rsrc_t ro = make_rsrc(p.out + m0 * p.ldo + n0,
-                                              (uint32_t)(((rows - 1) * p.ldo + cols) * 2));
-  const bool sw_vector = p.sw_step != 0;
-  const float sw0 = reinterpret_cast<const float*>(vec)[0];
-  float sam[MB];
-  static_for<MB>([&](auto mb) {
-    sam[mb] = p.sa ? reinterpret_cast<const float*>(vec + 1024)[wm * WM + mb * 32 + fr] : 1.0f;
-  });
-  auto body = [&](auto has_bias) {
-    static_for<NB>([&](auto nb) {
-      float sv[4][4], bv[4][4];
-      static_for<4>([&](auto g) {
-        const int col = wn * WN + nb * 32 + g * 8 + fh * 4;
-        const v4f s4 = *reinterpret_cast<const v4f*>(vec + col * 4);
-        uint2 b4 = make_uint2(0u, 0u);
-        if constexpr (has_bias) b4 = *reinterpret_cast<const uint2*>(vec + 2048 + col * 2);
-        static_for<4>([&](auto i) {
-          sv[g][i] = sw_vector ? s4[(int)i] : sw0;
-          const uint32_t bw = i < 2 ? b4.x : b4.y;
-          bv[g][i] = i % 2 ? bf16_hi(bw) : bf16_lo(bw);
-        });
-      });
-      static_for<MB>([&](auto mb) {
-        const int row = wm * WM + mb * 32 + fr;
-        uint32_t w[4][2];
-        static_for<4>([&](auto g) {
-          static_for<2>([&](auto h) {
-            constexpr int i0 = 2 * h, i1 = 2 * h + 1;
-            uint32_t pw = pack_bf16x2(acc[nb][mb][g * 4 + i0] * sam[mb] * sv[g][i0],
-                                      acc[nb][mb][g * 4 + i1] * sam[mb] * sv[g][i1]);
-            if constexpr (has_bias)
-              pw = pack_bf16x2(bf16_lo(pw) + bv[g][i0], bf16_hi(pw) + bv[g][i1]);
-            w[g][h] = pw;
-          });
-        });
-        static_for<2>([&](auto q) {
-          const auto x0 = __builtin_amdgcn_permlane32_swap(w[2 * q][0], w[2 * q + 1][0], false, false);
-          const auto x1 = __builtin_amdgcn_permlane32_swap(w[2 * q][1], w[2 * q + 1][1], false, false);
-          const v4i out = v4i{(int)x0[0], (int)x1[0], (int)x0[1], (int)x1[1]};
-          const int col = wn * WN + nb * 32 + 16 * q + 8 * fh;
-          const uint32_t off = col < cols ? (uint32_t)((row * p.ldo + col) * 2) : VFA_OOB;
-          __builtin_amdgcn_raw_buffer_store_b128(out, ro, (int)off, 0, 0);
-        });
-      });
-    });
-  };
-  if (p.bias) body(std::true_type{});
-  else body(std::false_type{});
 }
 
 }  // namespace vfa

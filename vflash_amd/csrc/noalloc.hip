@@ -89,7 +89,6 @@ int vflash_fp8_linear_swiglu_quantize_noalloc(const void* a, const float* sa, in
   p.amax_part = part_max;
   p.lora_scale = 1.0f;
   p.lora_strength = 1.0f;
-  p.group_m = 2;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (vfa::launch_fp8_gemm(p, vfa::EPI_SWIGLU, s) != hipSuccess) return VFLASH_ELAUNCH;
   return vfa::launch_requant_rows(static_cast<const uint16_t*>(h), m, n / 2, ldh, part_max,
