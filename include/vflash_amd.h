@@ -217,20 +217,22 @@ int vflash_fp8_linear_gate_residual(const void* a, const float* sa, int64_t lda,
  *   (src/vflash/adapters/h3_reference_lora.py:80-82).
  *   x bf16 [m, k] (ldx);  lora_a bf16 [rank, k] contiguous;  t bf16 [m, rank] contiguous
  *   Requires rank % 16 == 0, rank <= 128, k % 16 == 0, ldx % 8 == 0.
+ * Sum order: K is cut into 8 chunks of 32-element steps, [S c / 8, S (c + 1) / 8)
+ * with S = ceil(k / 32), each accumulated from zero; t = bf16 of the chunk
+ * sums added in chunk order.  The order depends on k only, never on m.
  */
 int vflash_lora_down(const void* x, int64_t m, int64_t k, int64_t ldx, const void* lora_a,
                      int64_t rank, void* t, void* stream);
 
 /*
  * Per-token E4M3 quantization and the LoRA down-projection of the same rows in
- * one pass, reading x once: the codes and scales of vflash_quantize_rows_e4m3
- * bit for bit, and t = bf16(x . A^T) summed in binary32 in another order than
- * vflash_lora_down (so t may differ from it in the last bf16 place).  Replaces
- * quantize_activation (src/vflash/native/h3_fp8_activation.py:12-55) plus the
- * adapter hook's inner F.linear (src/vflash/adapters/h3_reference_lora.py:80-82)
- * for the skinny adapter linears.
- *   Requires k % 16 == 0, k <= 2048, rank in {16, 32, 64}, rank * k <= 65536,
- *   ldx % 8 == 0; x, lora_a 16-byte aligned; codes, t 8-byte aligned.
+ * one launch: the codes and scales of vflash_quantize_rows_e4m3 bit for bit, and
+ * the t of vflash_lora_down bit for bit.  Replaces quantize_activation
+ * (src/vflash/native/h3_fp8_activation.py:12-55) plus the adapter hook's inner
+ * F.linear (src/vflash/adapters/h3_reference_lora.py:80-82) for the adapter
+ * linears.
+ *   Requires k % 16 == 0, rank % 16 == 0, 16 <= rank <= 128, ldx % 8 == 0,
+ *   m_pad >= m; x, lora_a 16-byte aligned; codes, t 8-byte aligned.
  */
 int vflash_quantize_rows_lora_e4m3(const void* x, int64_t m, int64_t k, int64_t ldx,
                                    void* codes, float* scales, int64_t m_pad,

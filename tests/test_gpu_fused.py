@@ -311,7 +311,8 @@ def test_lora_epilogue_under_each_tiling(dev, m, n, k, r):
 
 
 @pytest.mark.parametrize("m,k,r", [(1, 16, 16), (37, 1536, 32), (1024, 1536, 32), (300, 1024, 64),
-                                   (77, 528, 16), (9, 2048, 32)])
+                                   (77, 528, 16), (9, 2048, 32), (256, 5376, 128), (1000, 5376, 16),
+                                   (33, 48, 112)])
 def test_fused_quantize_and_lora_down_against_the_separate_kernels(dev, m, k, r):
     g = torch.Generator().manual_seed(m * 7 + k + r)
     x = (torch.randn((m, k), generator=g) * torch.rand((m, 1), generator=g) * 8).to(torch.bfloat16)
@@ -323,14 +324,11 @@ def test_fused_quantize_and_lora_down_against_the_separate_kernels(dev, m, k, r)
     ref_codes, ref_scales = kernels.quantize_rows(d(x))
     assert torch.equal(codes.view(torch.uint8), ref_codes.view(torch.uint8))
     assert torch.equal(scales, ref_scales)
-    # t: binary32 sums in another order, rounded to bf16 once.  Mostly the same
-    # bits; where the dot product cancels, the two orders differ by a few binary32
-    # ulps of the summands, which the rms term of rel_check covers.
-    t_sep = kernels.lora_down(d(x), d(la)).float().cpu().numpy()
-    t_one = t.float().cpu().numpy()
-    assert (t_one == t_sep).mean() > 0.98
-    rel_check(t_one, t_sep)
-    rel_check(t_one, O.lora_delta(x.float().numpy(), la.float().numpy(), np.eye(r, dtype=np.float32)))
+    # t: the same K chunks summed in the same order as the separate kernel.
+    t_sep = kernels.lora_down(d(x), d(la))
+    assert torch.equal(t, t_sep)
+    rel_check(t.float().cpu().numpy(),
+              O.lora_delta(x.float().numpy(), la.float().numpy(), np.eye(r, dtype=np.float32)))
     # And the codes against the oracle (padding rows included).
     oc, osc = O.quantize_rows(x.float().numpy())
     assert np.array_equal(u8(codes), oc) and np.array_equal(scales.reshape(-1).cpu().numpy(), osc)

@@ -251,8 +251,8 @@ int vflash_quantize_rows_lora_e4m3(const void* x, int64_t m, int64_t k, int64_t 
                                    void* codes, float* scales, int64_t m_pad,
                                    const void* lora_a, int64_t rank, void* t, void* stream) {
   if (!x || !codes || !scales || !lora_a || !t || m < 1 || m_pad < m) return VFLASH_EINVAL;
-  if (k < 16 || k % 16 || k > 2048 || ldx < k || ldx % 8) return VFLASH_EINVAL;
-  if ((rank != 16 && rank != 32 && rank != 64) || rank * k > 65536) return VFLASH_EINVAL;
+  if (k < 16 || k % 16 || ldx < k || ldx % 8) return VFLASH_EINVAL;
+  if (rank < 16 || rank > 128 || rank % 16) return VFLASH_EINVAL;
   if (!aligned(x, 16) || !aligned(lora_a, 16) || !aligned(t, 8) || !aligned(codes, 8) ||
       !aligned(scales, 4))
     return VFLASH_EINVAL;

@@ -293,13 +293,13 @@ def lora_down(x, lora_a):
 
 
 def quantize_lora_supported(k: int, rank: int) -> bool:
-    """Shapes of the one-pass quantize + LoRA-down kernel."""
-    return k % 16 == 0 and 16 <= k <= 2048 and rank in (16, 32, 64) and rank * k <= 65536
+    """Shapes of the fused quantize + LoRA-down kernel (those of ``lora_down``)."""
+    return k % 16 == 0 and k >= 16 and rank % 16 == 0 and 16 <= rank <= 128
 
 
 def quantize_rows_lora(x, lora_a, pad_to: int = 16):
-    """Codes/scales of ``quantize_rows(x)`` (bit-identical) and ``t = bf16(x lora_a^T)``
-    from one pass over ``x``; see ``quantize_lora_supported`` for the shapes."""
+    """Codes/scales of ``quantize_rows(x)`` and the ``t`` of ``lora_down(x, lora_a)``
+    (both bit-identical) from one launch; see ``quantize_lora_supported`` for the shapes."""
     if x.dtype != torch.bfloat16 or x.ndim != 2 or x.stride(1) != 1:
         raise ValueError("LoRA input must be a 2-D BF16 matrix with unit column stride")
     if lora_a.dtype != torch.bfloat16 or lora_a.ndim != 2 or not lora_a.is_contiguous():
