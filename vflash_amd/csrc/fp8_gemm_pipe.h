@@ -198,10 +198,11 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
   constexpr int RD = 2 * (MB + NB);  // ds_read_b128 per K-substep
   static_assert(QA > 0, "MFMAs after the barrier carry the DMA");
 
-  // Tiles of at most four 32x32 blocks per wave compute their adapter products
-  // before the K loop (64 registers); larger tiles, whose registers hold the
-  // main loop, compute them in the epilogue.
-  constexpr bool LORA_PRE = EPI == EPI_LORA && MB * NB <= 4;
+  // Tiles of at most eight 32x32 blocks per wave compute their adapter products
+  // before the K loop (up to 128 registers held through it), where the loads
+  // overlap the first stages' DMA; the 256x192 and 256x256 tiles, whose
+  // registers hold the main loop, compute them in the epilogue.
+  constexpr bool LORA_PRE = EPI == EPI_LORA && MB * NB <= 8;
   v16f lora_d[LORA_PRE ? MB * NB : 1];
   if constexpr (LORA_PRE) lora_blocks<BM, BN, WGM, WGN>(p, m0, n0, wm, wn, lane, lora_d);
   // Prologue and K loop; use_sdma selects the scalar-offset DMA (full tiles).

@@ -200,17 +200,27 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
         if (EPI == EPI_LORA && lora_d) {
           d = lora_d[nb * MB + mb];
         } else if constexpr (EPI == EPI_LORA) {
-          // delta block = B[n, :] . t[m, :] on bf16 MFMA, binary32 accumulate.
+          // delta block = B[n, :] . t[m, :] on bf16 MFMA, binary32 accumulate.  The
+          // operands of every rank step (rank <= 128) are loaded before the first
+          // MFMA, so a block waits for one memory round trip, not one per step.
           const int64_t nrow = n0 + wn * WN + nb * 32 + fr;
           const bool nok = nrow < p.n;
-          for (int r = 0; r < p.rank; r += 16) {
-            v8s bfr = v8s{}, tfr = v8s{};
-            if (nok) bfr = *reinterpret_cast<const v8s*>(p.lora_b + nrow * p.ldb + r + fh * 8);
-            if (mvalid) tfr = *reinterpret_cast<const v8s*>(p.lora_t + m * p.ldt + r + fh * 8);
-            d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, bfr),
-                                                        __builtin_bit_cast(v8bf, tfr), d, 0, 0,
-                                                        0);
-          }
+          v8s bfr[8], tfr[8];
+          static_for<8>([&](auto st) {
+            const bool live = st * 16 < p.rank;
+            bfr[st] = (live && nok) ? *reinterpret_cast<const v8s*>(p.lora_b + nrow * p.ldb +
+                                                                   st * 16 + fh * 8)
+                                    : v8s{};
+            tfr[st] = (live && mvalid) ? *reinterpret_cast<const v8s*>(p.lora_t + m * p.ldt +
+                                                                      st * 16 + fh * 8)
+                                       : v8s{};
+          });
+          static_for<8>([&](auto st) {
+            if (st * 16 < p.rank)
+              d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, bfr[st]),
+                                                          __builtin_bit_cast(v8bf, tfr[st]), d, 0,
+                                                          0, 0);
+          });
         }
         static_for<4>([&](auto g) {
           uint32_t w[2];
