@@ -60,6 +60,13 @@ def parse():
     p.add_argument("--operand-sets", type=int, default=0,
                    help="rotating operand sets for the small shapes (0 = enough to exceed the last-level cache)")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--operands", default="bench", choices=["bench", "constant", "random"],
+                   help="fp8_linear operands: the seeded configuration data (bench), constant codes "
+                        "(activations 448, weights 0.5), or uniformly random E4M3 codes; the GEMM "
+                        "does the same work on each, the board's power limit sets its clock")
+    p.add_argument("--board-power", action="store_true",
+                   help="after the timed steps, keep running the step and read the board's socket "
+                        "power and graphics clocks (amd-smi) while it runs")
     return p.parse_args()
 
 
@@ -285,6 +292,74 @@ def linear_sets(m, k, n, count, dev):
     return host, sets
 
 
+def operand_variant(kind, x, codes, scale, bias):
+    """The same linear on other operand bits (same shapes, scales and bias):
+    constant: every activation 1.0 (codes 448 after the per-token quantization)
+    and every weight code 0.5; random: uniformly drawn finite E4M3 codes for both
+    (each activation row holds 448, so its scale is 1 and its codes are the drawn
+    ones)."""
+    import torch
+
+    if kind == "constant":
+        return (torch.ones_like(x), torch.full_like(codes.view(torch.uint8), 0x30).view(codes.dtype),
+                scale, bias)
+    g = torch.Generator(device=x.device).manual_seed(7)
+
+    def draw(shape):
+        c = torch.randint(0, 254, shape, generator=g, device=x.device, dtype=torch.int32)
+        c = c + (c >= 127).to(torch.int32)  # skip 0x7f (NaN); 0xff is never drawn
+        return c.to(torch.uint8)
+
+    xa = draw(x.shape).view(torch.float8_e4m3fn).to(torch.bfloat16)
+    xa[:, 0] = 448.0
+    return (xa, draw(codes.shape).view(codes.dtype), scale, bias)
+
+
+def board_power(step, seconds=4.0):
+    """Run the step back to back for a few seconds while amd-smi reads the
+    socket power and the graphics clocks halfway through."""
+    import subprocess
+    import threading
+
+    import torch
+
+    result = {}
+
+    def query():
+        time.sleep(seconds / 2)
+        try:
+            r = subprocess.run(["amd-smi", "metric", "--power", "--clock"], capture_output=True,
+                               text=True, timeout=30)
+        except (OSError, subprocess.TimeoutExpired) as err:
+            result["error"] = str(err)[:200]
+            return
+        clocks, power = [], None
+        section = None
+        for line in r.stdout.splitlines():
+            t = line.strip()
+            if t.startswith("GFX_"):
+                section = "gfx"
+            elif t.endswith(":") and not t.startswith("GFX_"):
+                section = None if t != "POWER:" else "power"
+            if t.startswith("SOCKET_POWER:"):
+                power = t.split(":", 1)[1].strip()
+            elif section == "gfx" and t.startswith("CLK:"):
+                clocks.append(t.split(":", 1)[1].strip())
+        result.update({"tool": "amd-smi metric --power --clock", "socket_power": power,
+                       "gfx_clocks": clocks})
+
+    th = threading.Thread(target=query)
+    th.start()
+    i = 0
+    while th.is_alive():
+        for _ in range(10):
+            step(i, None)
+            i += 1
+        torch.cuda.synchronize()
+    th.join()
+    return result
+
+
 def make_workload(args, dev):
     import torch
 
@@ -296,6 +371,8 @@ def make_workload(args, dev):
         m, k, n = {"fp8_linear": (32760, 5120, 13824), "small": (4096, 3072, 3072),
                    "qkv": (32760, 5120, 15360)}[wl]
         host, sets = linear_sets(m, k, n, (args.operand_sets or 8) if wl == "small" else 1, dev)
+        if args.operands != "bench":
+            sets = [operand_variant(args.operands, *st) for st in sets]
         scope = ScopeTimer()
         ex = RowFP8Execution("w8a8", activation_quantizer="hip", measure=scope)
         from vflash_amd.fused import qkv_linear
@@ -317,6 +394,8 @@ def make_workload(args, dev):
                   if wl != "qkv" else "Merged QKV FP8 linear TFLOP/s (M=32760,K=5120,N=3x5120)")
         config = {"workload": names[wl], "m": m, "k": k, "n": n, "bias": True,
                   "activation_quant": "per-token e4m3 (HIP kernel)", "operand_sets": len(sets)}
+        if args.operands != "bench":
+            config["operands"] = args.operands
         if wl == "qkv":
             config["output"] = "3 planes [32760, 40 heads, 128]"
         cpu = None if args.no_cpu_baseline else (lambda: cpu_baseline_weight_only(*host, 2.0 * n * k))
@@ -717,6 +796,13 @@ def main():
             line["graph_rate"] = rate(w.work, graph, w.unit)
         except RuntimeError as err:  # a runtime that cannot capture the step
             line["graph_ms_per_step"] = {"error": str(err).splitlines()[0][:200]}
+    if args.operands != "bench":
+        line["data"] = {"constant": "synthetic: constant codes (activations 448 after quantization, "
+                                    "weights 0.5), seeded scales and bias",
+                        "random": "synthetic: uniformly random finite E4M3 codes for activations and "
+                                  "weights, seeded weight scales and bias"}[args.operands]
+    if args.board_power:
+        line["board"] = board_power(w.step)
     if device is not None:
         line["device_ms_per_step"] = device
         line["device_rate"] = rate(w.work, device, w.unit)

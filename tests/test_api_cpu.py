@@ -258,3 +258,31 @@ def test_bench_refuses_more_than_one_gpu():
     done = subprocess.run([sys.executable, str(bench), "--gpus", "2"], capture_output=True,
                           text=True, timeout=120)
     assert done.returncode != 0 and "one GPU" in done.stderr + done.stdout
+
+
+def test_bench_operand_variants_keep_the_shapes_and_finite_codes():
+    # The power-limit comparison runs the same GEMM on other operand bits:
+    # constant codes, or uniformly random finite E4M3 codes whose activation
+    # rows quantize with scale 1 to exactly the drawn codes.
+    import importlib.util
+    from pathlib import Path
+
+    spec = importlib.util.spec_from_file_location(
+        "bench_module", Path(__file__).resolve().parents[1] / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    from oracle import fp8 as O
+
+    x = torch.randn((48, 64)).to(torch.bfloat16)
+    codes = torch.zeros((32, 64), dtype=torch.uint8).view(torch.float8_e4m3fn)
+    scale, bias = torch.ones((32, 1)), torch.zeros(32, dtype=torch.bfloat16)
+    cx, cw, cs, cb = bench.operand_variant("constant", x, codes, scale, bias)
+    assert torch.equal(cx, torch.ones_like(x)) and bool((cw.view(torch.uint8) == 0x30).all())
+    assert cs is scale and cb is bias
+    rx, rw, _, _ = bench.operand_variant("random", x, codes, scale, bias)
+    assert rx.shape == x.shape and rw.shape == codes.shape
+    for c in (rw.view(torch.uint8), rx.float().to(torch.float8_e4m3fn).view(torch.uint8)):
+        assert not bool(((c & 0x7F) == 0x7F).any())  # no NaN code
+    qc, qs = O.quantize_rows(rx.float().numpy())
+    assert np.all(qs[:48] == 1.0)
+    assert np.array_equal(qc[:48], rx.float().to(torch.float8_e4m3fn).view(torch.uint8).numpy())
