@@ -11,6 +11,8 @@ Modules:
               gate-residual, LoRA), merged QKV
   nvfp4    -- NVFP4 packing, 128x4 scale order, activation quantization, W4A8 and W4A4 linears
   baseline -- the reference's CPU weight-only dequant-matmul path (torch)
+  fp8_torch -- fp8's rounding chains restated in torch for full-size checks on
+              the device, pinned bit for bit against fp8 on the CPU
 
 Pinning status of each function is stated in its docstring.
 """

@@ -68,3 +68,24 @@ def rel_check(actual, expected, rtol=1e-2):
     return float(np.max(err / denom)) if e.size else 0.0, float(np.mean(a == e)) if e.size else 1.0
 
 
+
+
+def rel_check_device(actual, expected, rtol=1e-2):
+    """rel_check for device tensors of the full configuration shapes (the same two
+    bounds, evaluated with torch in binary64 on the tensors' device).  Returns
+    (max_rel, exact_frac)."""
+    import torch
+
+    a = actual.double()
+    e = expected.double()
+    assert a.shape == e.shape
+    assert bool(torch.isfinite(a).all()), "non-finite kernel output"
+    rms = float(torch.sqrt(torch.mean(e * e))) if e.numel() else 0.0
+    err = (a - e).abs()
+    bound = rtol * e.abs() + rtol * rms
+    hard = int((err > 2.0**-6 * e.abs() + rtol * rms).sum())
+    assert hard == 0, f"{hard} of {e.numel()} beyond two bf16 ulps"
+    bad = int((err > bound).sum())
+    assert bad <= e.numel() // 10000, f"{bad} of {e.numel()} outside rtol={rtol}"
+    denom = torch.clamp(e.abs(), min=rms if rms > 0 else 1.0)
+    return float((err / denom).max()), float((a == e).double().mean())

@@ -5,7 +5,7 @@ import pytest
 import torch
 
 from oracle import fp8 as O
-from tests.conftest import rel_check
+from tests.conftest import rel_check, rel_check_device
 from vflash_amd import kernels
 from vflash_amd.fp8_linear import RowFP8Execution, RowFP8Linear
 from vflash_amd.fused import FusedQKV, fp8_ffn, fp8_linear_lora, merge_qkv, qkv_linear
@@ -53,6 +53,24 @@ def test_merged_qkv_config_shape_sampled(dev):
     ref = O.w8a8_linear(x.float().numpy()[rows], u8(w), s.reshape(-1).numpy(), b.float().numpy())
     got = np.concatenate([h.reshape(32760, 5120).float().cpu().numpy()[rows] for h in heads], axis=1)
     rel_check(got, ref)
+
+
+def test_merged_qkv_config_shape_every_element(dev):
+    # All 503 million outputs of the three planes against the oracle's chain
+    # restated in torch on the device (oracle/fp8_torch.py).
+    from oracle import fp8_torch as T
+
+    x, parts = qkv_inputs(32760, 5120, 5120)
+    ex = RowFP8Execution("w8a8", activation_quantizer="triton")
+    w, s = merge_qkv([p[0] for p in parts], [p[1] for p in parts])
+    b = (torch.randn(15360, generator=torch.Generator().manual_seed(7)) * 0.01).to(torch.bfloat16)
+    xd, wd, sd, bd = x.to(dev), w.to(dev), s.to(dev), b.to(dev)
+    q, k, v = qkv_linear(ex, xd, wd, sd, bd, planes=True)
+    ref = T.w8a8_linear(xd, wd, sd, bd)
+    for i, plane in enumerate((q, k, v)):
+        worst, exact = rel_check_device(plane, ref[:, 5120 * i:5120 * (i + 1)])
+        print(f"[qkv plane {i}] identical {exact:.6f}, worst {worst:.3g}")
+        assert exact > 0.95, (i, exact, worst)
 
 
 def test_fused_qkv_module_checks_its_parts(dev):
@@ -162,6 +180,82 @@ def test_ffn_config_shape_sampled(dev):
                       sd.reshape(-1).numpy(), bd.float().numpy(), gate.float().numpy(),
                       res.float().numpy()[rows])
     assert chain_error(got, chain) <= 1e-2
+
+
+def test_ffn_config_shape_every_element(dev):
+    # Every element of every stage at M=32760, 5120 -> 13824 -> 5120, against
+    # the oracle's chain restated in torch (oracle/fp8_torch.py): the up and down
+    # linears within the GEMM tolerance, GELU, the requantization and the
+    # gate-residual epilogue bit-exact on the kernel's own inputs to them.
+    from oracle import fp8_torch as T
+
+    m, h, f = 32760, 5120, 13824
+    x, cu, su, bu, cd, sd, bd, gate, res = ffn_inputs(m, h, f)
+    d = lambda t: t.to(dev)
+    xd, cud, sud, bud, cdd, sdd, bdd, gd, rd = map(d, (x, cu, su, bu, cd, sd, bd, gate, res))
+    a, sa = kernels.quantize_rows(xd)
+    y = kernels.fp8_gemm(a, sa, cud, sud, m, bud)
+    worst, exact = rel_check_device(y, T.w8a8_linear(xd, cud, sud, bud))
+    print(f"identical {exact:.6f}, worst {worst:.3g}")
+    assert exact > 0.95, (exact, worst)
+    hc, hs, g = kernels.gelu_quantize_rows(y, keep_values=True)
+    g_ref = T.gelu_tanh(y)
+    assert torch.equal(g.float().view(torch.int32), g_ref.view(torch.int32))
+    rc, rs = T.quantize_rows(g_ref)
+    assert torch.equal(hc.view(torch.uint8), rc) and torch.equal(hs.reshape(-1), rs)
+    del g, g_ref
+    check_down_projection(hc, hs, cdd, sdd, m, gd, rd, bdd)
+
+
+def check_down_projection(hc, hs, cd, sd, m, gate, res, bias):
+    """The output projection with its gate-residual epilogue at every element:
+    the projection (the plain bias epilogue on the same codes runs the same MFMA
+    chain) within the GEMM tolerance of the restated oracle, and the epilogue
+    bit-exact against the oracle's gate-residual rounding chain applied to it.
+    (The residual sum can cancel, so a tolerance relative to the final output
+    would not bound the projection.)"""
+    from oracle import fp8_torch as T
+
+    out = kernels.fp8_gemm_gate_residual(hc, hs, cd, sd, m, gate, res, bias)
+    y = kernels.fp8_gemm(hc, hs, cd, sd, m, bias)
+    worst, exact = rel_check_device(y, T.add_bias(T.scaled_mm(hc[:m], hs[:m], cd, sd), bias))
+    print(f"down projection identical {exact:.6f}, worst {worst:.3g}")
+    assert exact > 0.95, (exact, worst)
+    assert torch.equal(out.float().view(torch.int32), T.gate_residual(res, gate, y).view(torch.int32))
+
+
+def test_swiglu_h3_shape_every_element(dev):
+    # The H3 feed-forward (hidden 5376, inner 14336) at 32760 tokens: the SwiGLU
+    # tile's output against SwiGLU of the restated oracle linear (value and gate
+    # each within the GEMM bound, composed through one product), the row maxima
+    # and the requantization exact on the kernel's own h, and the output
+    # projection with its gate-residual within the GEMM tolerance.
+    from oracle import fp8_torch as T
+
+    m, h, f = 32760, 5376, 14336
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn((m, h), generator=g).to(torch.bfloat16)
+    cu, su = quantize_weight_rows(torch.randn((2 * f, h), generator=g) * 0.02)
+    bu = (torch.randn(2 * f, generator=g) * 0.01).to(torch.bfloat16)
+    cd, sd = quantize_weight_rows(torch.randn((h, f), generator=g) * 0.02)
+    bd = (torch.randn(h, generator=g) * 0.01).to(torch.bfloat16)
+    gate = torch.rand(h, generator=g).to(torch.bfloat16)
+    res = torch.randn((m, h), generator=g).to(torch.bfloat16)
+    d = lambda t: t.to(dev)
+    xd, cud, sud, bud, cdd, sdd, bdd, gd, rd = map(d, (x, cu, su, bu, cd, sd, bd, gate, res))
+    a, sa = kernels.quantize_rows(xd)
+    hh, amax = kernels.fp8_gemm_swiglu(a, sa, cud, sud, m, bud)
+    ref_h = T.silu_mul(T.w8a8_linear(xd, cud, sud, bud))
+    err = (hh.double() - ref_h.double()).abs()
+    rms = float(torch.sqrt(torch.mean(ref_h.double() ** 2)))
+    assert bool((err <= 2.0**-5 * ref_h.double().abs() + 1e-2 * rms).all())
+    assert float((err > 1e-2 * ref_h.double().abs() + 1e-2 * rms).double().mean()) <= 1e-3
+    del err, ref_h
+    assert torch.equal(amax, hh.float().abs().reshape(m, -1, 128).amax(dim=2))
+    hc, hs = kernels.requant_rows(hh, amax)
+    rc, rs = T.quantize_rows(hh)
+    assert torch.equal(hc.view(torch.uint8), rc) and torch.equal(hs.reshape(-1), rs)
+    check_down_projection(hc, hs, cdd, sdd, m, gd, rd, bdd)
 
 
 def within_one_ulp(got, ref):

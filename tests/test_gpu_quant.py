@@ -334,3 +334,18 @@ def test_portable_mode_keeps_torchs_scalar_division_on_the_gpu(dev):
     assert np.array_equal(portable.reshape(-1)[:rows].cpu().numpy().view(np.uint32), product.view(np.uint32))
     assert np.array_equal(fused.reshape(-1)[:rows].cpu().numpy().view(np.uint32), quotient.view(np.uint32))
     assert int((product != quotient).sum()) == 17410
+
+
+def test_oracle_restatement_rounds_like_the_oracle_on_the_device(dev):
+    # oracle/fp8_torch.py checks full-size outputs on the device: its bf16
+    # rounding must be the numpy oracle's there too, exact ties included.
+    from oracle import formats as F
+    from oracle import fp8_torch as T
+
+    rng = np.random.default_rng(5)
+    base = F.bf16_round(rng.standard_normal(50000) * np.exp2(rng.integers(-135, 120, 50000)))
+    base = base[np.isfinite(base) & (base != 0)].astype(np.float64)
+    half = np.exp2(np.floor(np.log2(np.abs(base))).clip(min=-126) - 8)
+    x = np.concatenate([base + np.sign(base) * half, rng.standard_normal(50000), [0.0, -0.0]])
+    got = T.bf16_round(torch.from_numpy(x).to(dev)).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), F.bf16_round(x).view(np.uint32))
