@@ -144,7 +144,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
   // Chunk c of staged row r sits in slot c ^ (r % SWZ): every slot of a row
   // when CH is a power of two, else within its aligned group of 8 (CH = 24).
   constexpr int SWZ = (CH & (CH - 1)) == 0 ? CH : 8;
-  static_assert(CH % SWZ == 0, "swizzle stays inside the row");
+  static_assert(CH % SWZ == 0 && (SWZ & (SWZ - 1)) == 0, "swizzle stays inside the row");
   constexpr int PITCH = BN * 2;
   const int lane = tid & 63, fr = lane & 31, fh = lane >> 5;
   const float* __restrict__ sa_p = p.sa;
@@ -242,7 +242,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
             w[h] = pw;
           });
           const int c = (wn * WN + nb * 32 + g * 8) / 8;  // 16-byte chunk of the row
-          *reinterpret_cast<uint2*>(stage + row * PITCH + ((c ^ (row % SWZ)) << 4) + fh * 8) =
+          *reinterpret_cast<uint2*>(stage + row * PITCH + ((c ^ (row & (SWZ - 1))) << 4) + fh * 8) =
               make_uint2(w[0], w[1]);
         });
       });
@@ -272,7 +272,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
     for (int it = 0; it < BM / RPO; ++it) {
       const int row = r0 + it * RPO;
       const bool valid = row < rows;
-      const int rs = row % SWZ;
+      const int rs = row & (SWZ - 1);
       const v4i vv = *reinterpret_cast<const v4i*>(stage + row * PITCH + ((c ^ rs) << 4));
       const v4i gg = *reinterpret_cast<const v4i*>(stage + row * PITCH + (((c + CHO) ^ rs) << 4));
       v4i h;
@@ -317,44 +317,130 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
     const int64_t plane = n / p.plane_cols;
     base = p.out + plane * p.plane_stride + (n - plane * p.plane_cols);
   }
+  // Chunk c of staged row `row` (SWZ is a power of two).
+  auto lds_chunk = [&](int row) {
+    return *reinterpret_cast<const v4i*>(stage + row * PITCH + ((c ^ (row & (SWZ - 1))) << 4));
+  };
+  // EPI_GATE: the residual chunk and the gate chunk of output row m0 + row,
+  // whose gate row is that of token `tok` (m % gate_tokens), through the index
+  // when one is given (the adaLN gather read in place).  An index outside
+  // [0, gate_rows) makes the row's gate NaN; nothing outside is read.  With
+  // unit gate stride and 16-byte aligned rows (vec_in) each is one load.
+  struct GateIn {
+    v4i res, gate;
+    float bad;
+  };
+  const bool vec_in = EPI == EPI_GATE && p.gate_hs == 1 &&
+                      ((reinterpret_cast<uintptr_t>(p.gate) | reinterpret_cast<uintptr_t>(p.residual)) & 15) == 0 &&
+                      p.gate_ts % 8 == 0 && p.ldr % 8 == 0;
+  auto gate_in = [&](int row, int64_t tok, auto vec) {
+    GateIn in;
+    const int64_t m = m0 + row;
+    int64_t g = tok;
+    in.bad = 0.0f;
+    if (p.gate_index) {
+      g = p.gate_index[tok];
+      if ((uint64_t)g >= (uint64_t)p.gate_rows) {
+        g = 0;
+        in.bad = __builtin_nanf("");
+      }
+    }
+    const uint16_t* res = p.residual + m * p.ldr + n;
+    const uint16_t* gt = p.gate + g * p.gate_ts + n * p.gate_hs;
+    if constexpr (vec) {
+      in.res = *reinterpret_cast<const v4i*>(res);
+      in.gate = *reinterpret_cast<const v4i*>(gt);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        in.res[j] = (int)((uint32_t)res[2 * j] | ((uint32_t)res[2 * j + 1] << 16));
+        in.gate[j] = (int)((uint32_t)gt[(2 * j) * p.gate_hs] |
+                           ((uint32_t)gt[(2 * j + 1) * p.gate_hs] << 16));
+      }
+    }
+    return in;
+  };
+  // out = bf16(residual + bf16(gate * y)) for the 8 outputs of a chunk.
+  auto gate_apply = [&](v4i v, const GateIn& in) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t y = (uint32_t)v[j], gw = (uint32_t)in.gate[j], rw = (uint32_t)in.res[j];
+      const uint32_t gy = pack_bf16x2((bf16_lo(gw) + in.bad) * bf16_lo(y),
+                                      (bf16_hi(gw) + in.bad) * bf16_hi(y));
+      v[j] = (int)pack_bf16x2(bf16_lo(rw) + bf16_lo(gy), bf16_hi(rw) + bf16_hi(gy));
+    }
+    return v;
+  };
+  auto store = [&](v4i v, uint16_t* dst, auto vec_out) {
+    if constexpr (vec_out) {
+      *reinterpret_cast<v4i*>(dst) = v;
+    } else {
+      reinterpret_cast<uint2*>(dst)[0] = make_uint2((uint32_t)v[0], (uint32_t)v[1]);
+      reinterpret_cast<uint2*>(dst)[1] = make_uint2((uint32_t)v[2], (uint32_t)v[3]);
+    }
+  };
+  // Token of row r0 (EPI_GATE), advanced by RPP rows per pass.
+  const int64_t tokens = EPI == EPI_GATE ? p.gate_tokens : 1;
+  int64_t tok = EPI == EPI_GATE ? (m0 + r0) % tokens : 0;
+  const int64_t tok_step = EPI == EPI_GATE ? RPP % tokens : 0;
+  auto next_tok = [&]() {
+    tok += tok_step;
+    if (tok >= tokens) tok -= tokens;
+  };
   auto pass = [&](auto vec_out) {
-#pragma unroll 8
-    for (int it = 0; it < PASSES; ++it) {
-      const int row = r0 + it * RPP;
-      if (row >= rows) break;
-      const int64_t m = m0 + row;
-      v4i v = *reinterpret_cast<const v4i*>(stage + row * PITCH + ((c ^ (row % SWZ)) << 4));
-      if constexpr (EPI == EPI_GATE) {
-        const uint16_t* res = p.residual + m * p.ldr + n;
-        // Gate row of output row m: token m % gate_tokens, through the index when
-        // one is given (the adaLN gather read in place).  An index outside
-        // [0, gate_rows) makes the row's gate NaN; nothing outside is read.
-        int64_t g = m % p.gate_tokens;
-        float bad = 0.0f;
-        if (p.gate_index) {
-          g = p.gate_index[g];
-          if ((uint64_t)g >= (uint64_t)p.gate_rows) {
-            g = 0;
-            bad = __builtin_nanf("");
+    if (rows == BM && (EPI != EPI_GATE || vec_in)) {
+      // A whole tile (with vector residual and gate loads for EPI_GATE): the
+      // chunks of BATCH rows (and their residual and gate chunks) are loaded
+      // before any is stored, so each latency is paid once
+      // per batch, not once per row.  The swizzle of row r0 + it * RPP repeats
+      // every four passes, so four LDS offsets and one output row step serve
+      // every pass.  Rows past BM (CH = 24: 26 passes of 10 rows) read inside
+      // the ring and are neither loaded from global memory nor stored.
+      static_assert((4 * RPP) % SWZ == 0, "the swizzle repeats every four passes");
+      constexpr int BATCH = PASSES < 8 ? PASSES : 8;
+      int lofs[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) lofs[k] = r0 * PITCH + ((c ^ ((r0 + k * RPP) & (SWZ - 1))) << 4);
+      uint16_t* const dst0 = base + (m0 + r0) * p.ldo;
+      const int64_t dstep = (int64_t)RPP * p.ldo;
+#pragma unroll
+      for (int it0 = 0; it0 < PASSES; it0 += BATCH) {
+        v4i v[BATCH];
+        GateIn in[BATCH];
+#pragma unroll
+        for (int j = 0; j < BATCH; ++j) {
+          const int it = it0 + j;
+          const int row = r0 + it * RPP;
+          v[j] = *reinterpret_cast<const v4i*>(stage + lofs[it & 3] + it * RPP * PITCH);
+          if constexpr (EPI == EPI_GATE) {
+            if (it < PASSES && (PASSES * RPP == BM || row < BM))
+              in[j] = gate_in(row, tok, std::true_type{});
+            next_tok();
           }
         }
-        const uint16_t* gt = p.gate + g * p.gate_ts + n * p.gate_hs;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t y = (uint32_t)v[j];
-          const uint32_t gy =
-              pack_bf16x2((bf16_to_f32(gt[(2 * j) * p.gate_hs]) + bad) * bf16_lo(y),
-                          (bf16_to_f32(gt[(2 * j + 1) * p.gate_hs]) + bad) * bf16_hi(y));
-          v[j] = (int)pack_bf16x2(bf16_to_f32(res[2 * j]) + bf16_lo(gy),
-                                  bf16_to_f32(res[2 * j + 1]) + bf16_hi(gy));
+        for (int j = 0; j < BATCH; ++j) {
+          const int it = it0 + j;
+          const int row = r0 + it * RPP;
+          if (it < PASSES && (PASSES * RPP == BM || row < BM)) {
+            v4i o = v[j];
+            if constexpr (EPI == EPI_GATE) o = gate_apply(o, in[j]);
+            store(o, dst0 + it * dstep, vec_out);
+          }
         }
       }
-      uint16_t* dst = base + m * p.ldo;
-      if constexpr (vec_out) {
-        *reinterpret_cast<v4i*>(dst) = v;
-      } else {
-        reinterpret_cast<uint2*>(dst)[0] = make_uint2((uint32_t)v[0], (uint32_t)v[1]);
-        reinterpret_cast<uint2*>(dst)[1] = make_uint2((uint32_t)v[2], (uint32_t)v[3]);
+    } else {
+#pragma unroll 8
+      for (int it = 0; it < PASSES; ++it) {
+        const int row = r0 + it * RPP;
+        if (row >= rows) break;
+        v4i o = lds_chunk(row);
+        if constexpr (EPI == EPI_GATE) {
+          o = vec_in ? gate_apply(o, gate_in(row, tok, std::true_type{}))
+                     : gate_apply(o, gate_in(row, tok, std::false_type{}));
+          next_tok();
+        }
+        store(o, base + (m0 + row) * p.ldo, vec_out);
       }
     }
   };
