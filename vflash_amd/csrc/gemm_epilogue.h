@@ -268,33 +268,55 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
     const int rows = (int)min((int64_t)BM, p.m - m0);
     const int parts = (int)((p.half_n + BN / 2 - 1) / (BN / 2));
     const int part = (int)(n0 / (BN / 2));
-#pragma unroll 4
-    for (int it = 0; it < BM / RPO; ++it) {
-      const int row = r0 + it * RPO;
-      const bool valid = row < rows;
-      const int rs = row & (SWZ - 1);
-      const v4i vv = *reinterpret_cast<const v4i*>(stage + row * PITCH + ((c ^ rs) << 4));
-      const v4i gg = *reinterpret_cast<const v4i*>(stage + row * PITCH + (((c + CHO) ^ rs) << 4));
-      v4i h;
-      uint32_t amax_pk = 0u;
+    // The swizzle of row r0 + it * RPO repeats every two passes: two LDS
+    // offsets per half serve every pass.  The chunks of a batch of rows are
+    // read before any is used, so the LDS latency is paid once per batch.
+    static_assert((2 * RPO) % SWZ == 0, "the swizzle repeats every two passes");
+    constexpr int PASSES = BM / RPO, BATCH = PASSES < 8 ? PASSES : 8;
+    // Output row r0 + it * RPO: one row step per pass for h and for the maxima.
+    uint16_t* const out0 = p.out + (m0 + r0) * p.ldo + n;
+    const int64_t ostep = (int64_t)RPO * p.ldo;
+    float* const amax0 = p.amax_part + (m0 + r0) * parts + part;
+    const int64_t astep = (int64_t)RPO * parts;
+    const bool full = rows == BM;
+    int vofs[2], gofs[2];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t vw = (uint32_t)vv[j], gw = (uint32_t)gg[j];
-        const float g0 = bf16_lo(gw), g1 = bf16_hi(gw);
-        const uint32_t sp = pack_bf16x2(silu_of_bf16(g0), silu_of_bf16(g1));
-        const uint32_t hw = pack_bf16x2(bf16_lo(vw) * bf16_lo(sp), bf16_hi(vw) * bf16_hi(sp));
-        amax_pk = abs_max_pk(amax_pk, hw);
-        h[j] = (int)hw;
+    for (int k = 0; k < 2; ++k) {
+      const int rs = (r0 + k * RPO) & (SWZ - 1);
+      vofs[k] = r0 * PITCH + ((c ^ rs) << 4);
+      gofs[k] = r0 * PITCH + (((c + CHO) ^ rs) << 4);
+    }
+#pragma unroll
+    for (int it0 = 0; it0 < PASSES; it0 += BATCH) {
+      v4i vv[BATCH], gg[BATCH];
+#pragma unroll
+      for (int j = 0; j < BATCH; ++j) {
+        const int it = it0 + j;
+        vv[j] = *reinterpret_cast<const v4i*>(stage + vofs[it & 1] + it * RPO * PITCH);
+        gg[j] = *reinterpret_cast<const v4i*>(stage + gofs[it & 1] + it * RPO * PITCH);
       }
-      // Maximum over the 16 lanes of the 128-column group, NaN propagated.
-      uint32_t au = __float_as_uint(abs_max_value(amax_pk));
 #pragma unroll
-      for (int o = 8; o > 0; o >>= 1) au = max(au, (uint32_t)__shfl_xor((int)au, o, 64));
-      const float amax = __uint_as_float(au);
-      if (valid) {
-        const int64_t m = m0 + row;
-        if (n < p.half_n) *reinterpret_cast<v4i*>(p.out + m * p.ldo + n) = h;
-        if (c == 0) p.amax_part[m * parts + part] = amax;
+      for (int j = 0; j < BATCH; ++j) {
+        const int row = r0 + (it0 + j) * RPO;
+        v4i h;
+        uint32_t amax_pk = 0u;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t vw = (uint32_t)vv[j][q], gw = (uint32_t)gg[j][q];
+          const float g0 = bf16_lo(gw), g1 = bf16_hi(gw);
+          const uint32_t sp = pack_bf16x2(silu_of_bf16(g0), silu_of_bf16(g1));
+          const uint32_t hw = pack_bf16x2(bf16_lo(vw) * bf16_lo(sp), bf16_hi(vw) * bf16_hi(sp));
+          amax_pk = abs_max_pk(amax_pk, hw);
+          h[q] = (int)hw;
+        }
+        // Maximum over the 16 lanes of the 128-column group (one DPP row),
+        // NaN propagated: the bit patterns of |h| compare as unsigned integers.
+        const float amax = __uint_as_float(row16_max_u32(__float_as_uint(abs_max_value(amax_pk))));
+        const int it = it0 + j;
+        if (full || row < rows) {
+          if (n < p.half_n) *reinterpret_cast<v4i*>(out0 + it * ostep) = h;
+          if (c == 0) amax0[it * astep] = amax;
+        }
       }
     }
     return;
