@@ -222,6 +222,21 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
                                                           0, 0);
           });
         }
+        if constexpr (EPI == EPI_LORA) {
+          // delta = bf16(t . B^T), then the optional bf16(delta * scale) and
+          // bf16(delta * strength) steps, for the block's 16 values at once (two
+          // uniform branches per block); d then holds bf16 values as binary32.
+          auto round_pairs = [&](float f) {
+            static_for<8>([&](auto i) {
+              const uint32_t dp = pack_bf16x2(d[2 * i] * f, d[2 * i + 1] * f);
+              d[2 * i] = bf16_lo(dp);
+              d[2 * i + 1] = bf16_hi(dp);
+            });
+          };
+          round_pairs(1.0f);
+          if (p.lora_scale != 1.0f) round_pairs(p.lora_scale);
+          if (p.lora_strength != 1.0f) round_pairs(p.lora_strength);
+        }
         static_for<4>([&](auto g) {
           uint32_t w[2];
           // Output pairs: every bf16 rounding is one v_cvt_pk_bf16_f32 for two values.
@@ -231,14 +246,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
                                       acc[nb][mb][g * 4 + i1] * sam[mb] * sv[g][i1]);
             if constexpr (has_bias)
               pw = pack_bf16x2(bf16_lo(pw) + bv[g][i0], bf16_hi(pw) + bv[g][i1]);
-            if constexpr (EPI == EPI_LORA) {
-              uint32_t dp = pack_bf16x2(d[g * 4 + i0], d[g * 4 + i1]);
-              if (p.lora_scale != 1.0f)
-                dp = pack_bf16x2(bf16_lo(dp) * p.lora_scale, bf16_hi(dp) * p.lora_scale);
-              if (p.lora_strength != 1.0f)
-                dp = pack_bf16x2(bf16_lo(dp) * p.lora_strength, bf16_hi(dp) * p.lora_strength);
-              pw = pack_bf16x2(bf16_lo(pw) + bf16_lo(dp), bf16_hi(pw) + bf16_hi(dp));
-            }
+            if constexpr (EPI == EPI_LORA)
+              pw = pack_bf16x2(bf16_lo(pw) + d[g * 4 + i0], bf16_hi(pw) + d[g * 4 + i1]);
             w[h] = pw;
           });
           const int c = (wn * WN + nb * 32 + g * 8) / 8;  // 16-byte chunk of the row
