@@ -496,3 +496,33 @@ def test_ffn_with_gate_index_equals_the_gathered_gate(dev):
     got = fp8_ffn(*args, table[:, 5, :], d(res), activation="swiglu", gate_index=index)
     ref = fp8_ffn(*args, table[:, 5, :].index_select(0, index).repeat(2, 1), d(res), activation="swiglu")
     assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("m,h,k", [(300, 512, 384), (4096, 5120, 256)])
+def test_gate_residual_operand_layouts_give_the_same_bits(dev, m, h, k):
+    # The epilogue loads a residual and a gate chunk with one 16-byte load each
+    # when both are 16-byte aligned and the gate has unit column stride, and
+    # element by element otherwise; the output takes 16-byte stores when it is
+    # aligned.  Every layout computes the same bits.  The shapes cover whole
+    # and partial 64x64 tiles and the 256x192 tiling's rows past the tile.
+    g = torch.Generator().manual_seed(61)
+    x = torch.randn((m, k), generator=g).to(torch.bfloat16).to(dev)
+    cw, sw = quantize_weight_rows(torch.randn((h, k), generator=g) * 0.02)
+    cw, sw = cw.to(dev), sw.to(dev)
+    bias = (torch.randn(h, generator=g) * 0.01).to(torch.bfloat16).to(dev)
+    res = torch.randn((m, h), generator=g).to(torch.bfloat16).to(dev)
+    gate = torch.rand((m, h), generator=g).to(torch.bfloat16).to(dev)
+    a, sa = kernels.quantize_rows(x)
+    run = lambda gt, rs, **kw: kernels.fp8_gemm_gate_residual(a, sa, cw, sw, m, gt, rs, bias, **kw)
+    ref = run(gate, res)
+    gate_cols = gate.t().contiguous().t()            # column stride m
+    wide = torch.empty((m, h + 1), dtype=torch.bfloat16, device=dev)
+    wide[:, 1:] = res
+    res_shifted = wide[:, 1:]                          # 2-byte aligned rows, stride h + 1
+    assert gate_cols.stride() == (1, m) and res_shifted.data_ptr() % 16
+    assert torch.equal(run(gate_cols, res), ref)
+    assert torch.equal(run(gate, res_shifted), ref)
+    out_buf = torch.empty((m, h + 4), dtype=torch.bfloat16, device=dev)
+    out = out_buf[:, :h]                               # rows 8-byte aligned only
+    run(gate_cols, res_shifted, out=out)
+    assert torch.equal(out, ref)

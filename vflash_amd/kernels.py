@@ -119,7 +119,8 @@ def fp8_gemm(codes, act_scale, weight, w_scale, rows, bias=None, out=None):
     n, k = weight.shape
     if out is None:
         out = torch.empty((rows, n), device=device, dtype=torch.bfloat16)
-    if out.dtype != torch.bfloat16 or out.shape != (rows, n) or out.stride(1) != 1:
+    if (out.dtype != torch.bfloat16 or out.shape != (rows, n) or out.stride(1) != 1
+            or out.device != device):
         raise ValueError("GEMM output must be BF16 [rows, N] with unit column stride")
     if rows:
         call("vflash_fp8_linear", ptr(codes), ptr(act_scale), codes.stride(0), ptr(weight),
@@ -266,6 +267,9 @@ def fp8_gemm_gate_residual(codes, act_scale, weight, w_scale, rows, gate, residu
     require_device(gate, residual, gate_index)
     if out is None:
         out = torch.empty((rows, n), device=device, dtype=torch.bfloat16)
+    elif (out.dtype != torch.bfloat16 or out.shape != (rows, n) or out.stride(1) != 1
+          or out.device != device):
+        raise ValueError("out must be a BF16 [rows, N] matrix with unit column stride")
     if rows:
         call("vflash_fp8_linear_gate_residual", ptr(codes), ptr(act_scale), codes.stride(0),
              ptr(weight), ptr(w_scale), weight.stride(0), rows, n, k, ptr(bias), ptr(gate), gts,
