@@ -199,8 +199,8 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
   static_assert(QA > 0, "MFMAs after the barrier carry the DMA");
 
   // Tiles of at most eight 32x32 blocks per wave compute their adapter products
-  // before the K loop (up to 128 registers held through it), where the loads
-  // overlap the first stages' DMA; the 256x192 and 256x256 tiles, whose
+  // before the K loop (up to 128 registers held through it), so the epilogue
+  // does not wait on their loads; the 256x192 and 256x256 tiles, whose
   // registers hold the main loop, compute them in the epilogue.
   constexpr bool LORA_PRE = EPI == EPI_LORA && MB * NB <= 8;
   v16f lora_d[LORA_PRE ? MB * NB : 1];
