@@ -1,0 +1,114 @@
+"""Seeded random shapes through every GEMM epilogue: each output within the
+tolerance of the oracle's rounding chain (its torch restatement, binary64 sums
+on the device), and every call split at a random row bit-identical to the
+whole call.  The shapes sweep M from 1 to several thousand rows and N and K
+over multiples of 16, so every tiling the shape rule picks, partial tiles in
+both directions and the multi-round grids all run."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8_torch as T
+from tests.conftest import rel_check_device
+from vflash_amd import kernels
+from vflash_amd.prepare import quantize_weight_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def shapes(seed, count):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(count):
+        m = int(rng.choice([1, 7, 16, 63, 200, 777, 1500, 4100, 9000]))
+        n = 16 * int(rng.integers(1, 400))
+        k = 16 * int(rng.integers(1, 200))
+        out.append((m, n, k))
+    return out
+
+
+def operands(dev, m, n, k, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((m, k), generator=g).to(torch.bfloat16).to(dev)
+    cw, sw = quantize_weight_rows(torch.randn((n, k), generator=g) * 0.05)
+    bias = (torch.randn(n, generator=g) * 0.1).to(torch.bfloat16).to(dev)
+    return x, cw.to(dev), sw.to(dev), bias
+
+
+def split_equal(run, m, split):
+    """run(lo, hi) computes rows [lo, hi); the two parts must equal the whole."""
+    whole = run(0, m)
+    if 0 < split < m:
+        parts = torch.cat([run(0, split), run(split, m)])
+        assert torch.equal(parts, whole)
+    return whole
+
+
+@pytest.mark.parametrize("m,n,k", shapes(5, 12))
+def test_linear_bias_random_shape(dev, m, n, k):
+    x, cw, sw, bias = operands(dev, m, n, k, m + n + k)
+    codes, sa = kernels.quantize_rows(x)
+    ref_codes, ref_sa = T.quantize_rows(x)
+    assert torch.equal(codes.view(torch.uint8), ref_codes) and torch.equal(sa.reshape(-1), ref_sa)
+
+    def run(lo, hi):
+        c, s = kernels.quantize_rows(x[lo:hi])
+        return kernels.fp8_gemm(c, s, cw, sw, hi - lo, bias)
+
+    out = split_equal(run, m, max(1, m // 3))
+    want = T.add_bias(T.scaled_mm(ref_codes[:m], ref_sa[:m], cw.view(torch.uint8), sw), bias)
+    rel_check_device(out, want)
+
+
+@pytest.mark.parametrize("m,n,k", shapes(6, 8))
+def test_gate_residual_random_shape(dev, m, n, k):
+    x, cw, sw, bias = operands(dev, m, n, k, 3 * m + n + k)
+    g = torch.Generator().manual_seed(m + 2 * n)
+    res = torch.randn((m, n), generator=g).to(torch.bfloat16).to(dev)
+    gate = torch.rand((m, n), generator=g).to(torch.bfloat16).to(dev)
+
+    def run(lo, hi):
+        c, s = kernels.quantize_rows(x[lo:hi])
+        return kernels.fp8_gemm_gate_residual(c, s, cw, sw, hi - lo, gate[lo:hi], res[lo:hi], bias)
+
+    out = split_equal(run, m, max(1, m // 2))
+    codes, sa = T.quantize_rows(x)
+    y = T.add_bias(T.scaled_mm(codes[:m], sa[:m], cw.view(torch.uint8), sw), bias)
+    # The projection is within the GEMM tolerance; the epilogue on the kernel's
+    # own projection is bit-exact.
+    c, s = kernels.quantize_rows(x)
+    y_k = kernels.fp8_gemm(c, s, cw, sw, m, bias)
+    rel_check_device(y_k, y)
+    assert torch.equal(out, T.gate_residual(res, gate, y_k).to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("m,n,k", shapes(7, 8))
+@pytest.mark.parametrize("rank", [16, 48])
+def test_lora_random_shape(dev, m, n, k, rank):
+    x, cw, sw, bias = operands(dev, m, n, k, 5 * m + n + k + rank)
+    g = torch.Generator().manual_seed(m + 7 * n + rank)
+    la = (torch.randn((rank, k), generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    lb = (torch.randn((n, rank), generator=g) * 0.05).to(torch.bfloat16).to(dev)
+
+    def run(lo, hi):
+        c, s = kernels.quantize_rows(x[lo:hi])
+        t = kernels.lora_down(x[lo:hi], la)
+        return kernels.fp8_gemm_lora(c, s, cw, sw, hi - lo, t, lb, scale=0.5, strength=1.25,
+                                     bias=bias)
+
+    out = split_equal(run, m, max(1, (2 * m) // 3))
+    # The fused quantization + down-projection gives the separate kernels' bits.
+    if kernels.quantize_lora_supported(k, rank):
+        c2, s2, t2 = kernels.quantize_rows_lora(x, la)
+        c1, s1 = kernels.quantize_rows(x)
+        assert torch.equal(c2.view(torch.uint8), c1.view(torch.uint8)) and torch.equal(s2, s1)
+        assert torch.equal(t2, kernels.lora_down(x, la))
+    # Within tolerance of the whole chain in binary64: base + bf16 rounded delta.
+    codes, sa = T.quantize_rows(x)
+    base = T.add_bias(T.scaled_mm(codes[:m], sa[:m], cw.view(torch.uint8), sw), bias)
+    t = T.bf16_round(x.double() @ la.double().T)
+    delta = T.bf16_round(T.bf16_round(T.bf16_round(t.double() @ lb.double().T).double() * 0.5)
+                         .double() * 1.25)
+    want = T.bf16_round(base.double() + delta.double())
+    rel_check_device(out, want)
