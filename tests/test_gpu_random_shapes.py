@@ -1,7 +1,7 @@
-"""Seeded random shapes through every GEMM epilogue: each output within the
-tolerance of the oracle's rounding chain (its torch restatement, binary64 sums
-on the device), and every call split at a random row bit-identical to the
-whole call.  The shapes sweep M from 1 to several thousand rows and N and K
+"""Seeded random shapes through every GEMM epilogue and the NVFP4 GEMMs: each
+FP8 output within the tolerance of the oracle's rounding chain (its torch
+restatement, binary64 sums on the device), and every call split at a row
+bit-identical to the whole call.  The shapes sweep M from 1 to several thousand rows and N and K
 over multiples of 16, so every tiling the shape rule picks, partial tiles in
 both directions and the multi-round grids all run."""
 
@@ -112,3 +112,75 @@ def test_lora_random_shape(dev, m, n, k, rank):
                          .double() * 1.25)
     want = T.bf16_round(base.double() + delta.double())
     rel_check_device(out, want)
+
+
+def shapes_multiple(seed, count, n_unit, k_unit, n_max, k_max):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(count):
+        m = int(rng.choice([1, 7, 63, 200, 777, 1500, 4100, 9000]))
+        out.append((m, n_unit * int(rng.integers(1, n_max // n_unit + 1)),
+                    k_unit * int(rng.integers(1, k_max // k_unit + 1))))
+    return out
+
+
+@pytest.mark.parametrize("m,n,k", shapes_multiple(8, 8, 256, 16, 8192, 3072))
+def test_swiglu_random_shape(dev, m, n, k):
+    x, cw, sw, bias = operands(dev, m, n, k, 7 * m + n + k)
+
+    def run(lo, hi):
+        c, s = kernels.quantize_rows(x[lo:hi])
+        h, amax = kernels.fp8_gemm_swiglu(c, s, cw, sw, hi - lo, bias)
+        return torch.cat([h.float(), amax], dim=1)
+
+    out = split_equal(run, m, max(1, m // 4))
+    f = n // 2
+    h, amax = out[:, :f], out[:, f:]
+    # The row maxima per 128 columns are those of the kernel's own h.
+    assert torch.equal(amax, h.abs().reshape(m, -1, 128).amax(dim=2))
+    # h is a product of two GEMM outputs (value and gate, each within the GEMM
+    # bound): every element within 2^-5 of the oracle's h plus 1 % of its rms,
+    # and at most 1 in 1000 beyond 1 % (the bound of the full-shape test).
+    codes, sa = T.quantize_rows(x)
+    base = T.add_bias(T.scaled_mm(codes[:m], sa[:m], cw.view(torch.uint8), sw), bias)
+    ref = T.silu_mul(base).double()
+    err = (h.double() - ref).abs()
+    rms = float(torch.sqrt(torch.mean(ref * ref)))
+    assert bool((err <= 2.0**-5 * ref.abs() + 1e-2 * rms).all())
+    assert float((err > 1e-2 * ref.abs() + 1e-2 * rms).double().mean()) <= 1e-3
+
+
+@pytest.mark.parametrize("m,n,k", shapes_multiple(9, 6, 48, 16, 6144, 2048))
+def test_planes_random_shape(dev, m, n, k):
+    x, cw, sw, bias = operands(dev, m, n, k, 11 * m + n + k)
+    c, s = kernels.quantize_rows(x)
+    whole = kernels.fp8_gemm(c, s, cw, sw, m, bias)
+
+    def run(lo, hi):
+        cc, ss = kernels.quantize_rows(x[lo:hi])
+        return kernels.fp8_gemm_planes(cc, ss, cw, sw, hi - lo, 3, bias).permute(1, 0, 2)
+
+    planes = split_equal(run, m, max(1, m // 3))
+    assert torch.equal(planes.reshape(m, n), whole)
+
+
+@pytest.mark.parametrize("m,n,k", shapes_multiple(10, 6, 128, 64, 4096, 4096))
+def test_nvfp4_random_shape(dev, m, n, k):
+    from vflash_amd.prepare import quantize_nvfp4_weight
+
+    g = torch.Generator().manual_seed(13 * m + n + k)
+    x = torch.randn((m, k), generator=g).to(torch.bfloat16).to(dev)
+    packed, scales, alpha, _ = quantize_nvfp4_weight((torch.randn((n, k), generator=g) * 0.05).to(dev))
+    bias = (torch.randn(n, generator=g) * 0.1).to(torch.bfloat16).to(dev)
+    gsf = torch.tensor(2688.0 / float(x.float().abs().amax()), device=dev)
+
+    def w4a8(lo, hi):
+        c, s = kernels.quantize_rows(x[lo:hi])
+        return kernels.nvfp4_gemm(c, s, packed, scales, alpha, hi - lo, bias)
+
+    def w4a4(lo, hi):
+        c, s = kernels.nvfp4_quantize_rows(x[lo:hi], gsf)
+        return kernels.nvfp4_w4a4_gemm(c, s, packed, scales, alpha / gsf, hi - lo, bias)
+
+    split_equal(w4a8, m, max(1, m // 2))
+    split_equal(w4a4, m, max(1, m // 3))
