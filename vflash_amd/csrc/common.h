@@ -54,6 +54,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return r;
 }
 
+// bf16(f) widened back to binary32 by one v_cvt_pk_bf16_f32: the rounded
+// value lands in the high half and zero in the low half, so no shift or mask
+// extracts it.
+__device__ __forceinline__ float round_bf16_wide(float f) {
+  uint32_t r;
+  asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(r) : "v"(f));
+  return __uint_as_float(r);
+}
+
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 

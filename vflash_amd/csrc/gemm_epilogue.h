@@ -227,11 +227,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
           // bf16(delta * strength) steps, for the block's 16 values at once (two
           // uniform branches per block); d then holds bf16 values as binary32.
           auto round_pairs = [&](float f) {
-            static_for<8>([&](auto i) {
-              const uint32_t dp = pack_bf16x2(d[2 * i] * f, d[2 * i + 1] * f);
-              d[2 * i] = bf16_lo(dp);
-              d[2 * i + 1] = bf16_hi(dp);
-            });
+            static_for<16>([&](auto i) { d[(int)i] = round_bf16_wide(d[(int)i] * f); });
           };
           round_pairs(1.0f);
           if (p.lora_scale != 1.0f) round_pairs(p.lora_scale);
@@ -242,13 +238,19 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
           // Output pairs: every bf16 rounding is one v_cvt_pk_bf16_f32 for two values.
           static_for<2>([&](auto h) {
             constexpr int i0 = 2 * h, i1 = 2 * h + 1;
-            uint32_t pw = pack_bf16x2(acc[nb][mb][g * 4 + i0] * sam[mb] * sv[g][i0],
-                                      acc[nb][mb][g * 4 + i1] * sam[mb] * sv[g][i1]);
-            if constexpr (has_bias)
-              pw = pack_bf16x2(bf16_lo(pw) + bv[g][i0], bf16_hi(pw) + bv[g][i1]);
-            if constexpr (EPI == EPI_LORA)
-              pw = pack_bf16x2(bf16_lo(pw) + d[g * 4 + i0], bf16_hi(pw) + d[g * 4 + i1]);
-            w[h] = pw;
+            // A rounding whose result is used again is one conversion per value
+            // (round_bf16_wide), the last one per pair.
+            float y0 = acc[nb][mb][g * 4 + i0] * sam[mb] * sv[g][i0];
+            float y1 = acc[nb][mb][g * 4 + i1] * sam[mb] * sv[g][i1];
+            if constexpr (has_bias) {
+              y0 = round_bf16_wide(y0) + bv[g][i0];
+              y1 = round_bf16_wide(y1) + bv[g][i1];
+            }
+            if constexpr (EPI == EPI_LORA) {
+              y0 = round_bf16_wide(y0) + d[g * 4 + i0];
+              y1 = round_bf16_wide(y1) + d[g * 4 + i1];
+            }
+            w[h] = pack_bf16x2(y0, y1);
           });
           const int c = (wn * WN + nb * 32 + g * 8) / 8;  // 16-byte chunk of the row
           *reinterpret_cast<uint2*>(stage + row * PITCH + ((c ^ (row & (SWZ - 1))) << 4) + fh * 8) =
@@ -355,11 +357,11 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
   // EPI_GATE: the residual chunk and the gate chunk of output row m0 + row,
   // whose gate row is that of token `tok` (m % gate_tokens), through the index
   // when one is given (the adaLN gather read in place).  An index outside
-  // [0, gate_rows) makes the row's gate NaN; nothing outside is read.  With
-  // unit gate stride and 16-byte aligned rows (vec_in) each is one load.
+  // [0, gate_rows) makes the row's gate NaN (quiet-NaN bf16 pairs in place of
+  // the gate chunk); nothing outside is read.  With unit gate stride and
+  // 16-byte aligned rows (vec_in) each is one load.
   struct GateIn {
     v4i res, gate;
-    float bad;
   };
   const bool vec_in = EPI == EPI_GATE && p.gate_hs == 1 &&
                       ((reinterpret_cast<uintptr_t>(p.gate) | reinterpret_cast<uintptr_t>(p.residual)) & 15) == 0 &&
@@ -368,12 +370,12 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
     GateIn in;
     const int64_t m = m0 + row;
     int64_t g = tok;
-    in.bad = 0.0f;
+    bool bad = false;
     if (p.gate_index) {
       g = p.gate_index[tok];
       if ((uint64_t)g >= (uint64_t)p.gate_rows) {
         g = 0;
-        in.bad = __builtin_nanf("");
+        bad = true;
       }
     }
     const uint16_t* res = p.residual + m * p.ldr + n;
@@ -389,6 +391,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
                            ((uint32_t)gt[(2 * j + 1) * p.gate_hs] << 16));
       }
     }
+    if (bad) in.gate = v4i{0x7fc07fc0, 0x7fc07fc0, 0x7fc07fc0, 0x7fc07fc0};
     return in;
   };
   // out = bf16(residual + bf16(gate * y)) for the 8 outputs of a chunk.
@@ -396,9 +399,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t y = (uint32_t)v[j], gw = (uint32_t)in.gate[j], rw = (uint32_t)in.res[j];
-      const uint32_t gy = pack_bf16x2((bf16_lo(gw) + in.bad) * bf16_lo(y),
-                                      (bf16_hi(gw) + in.bad) * bf16_hi(y));
-      v[j] = (int)pack_bf16x2(bf16_lo(rw) + bf16_lo(gy), bf16_hi(rw) + bf16_hi(gy));
+      const float gy0 = round_bf16_wide(bf16_lo(gw) * bf16_lo(y));
+      const float gy1 = round_bf16_wide(bf16_hi(gw) * bf16_hi(y));
+      v[j] = (int)pack_bf16x2(bf16_lo(rw) + gy0, bf16_hi(rw) + gy1);
     }
     return v;
   };
