@@ -13,6 +13,8 @@ import struct
 import subprocess
 import sys
 from concurrent.futures import ThreadPoolExecutor
+from decimal import Decimal, localcontext
+from fractions import Fraction
 from pathlib import Path
 
 PACKAGE = Path(__file__).resolve().parent
@@ -84,6 +86,99 @@ def gelu_tanh_bf16(bits: int) -> int:
     return _bf16_bits_of_double(x / (1.0 + math.exp(t)))
 
 
+F32_MAX = Fraction(struct.unpack("<f", struct.pack("<I", 0x7F7FFFFF))[0])
+
+
+def _f32_of_fraction(x: Fraction) -> float:
+    """A rational rounded to binary32 (nearest, ties to even; past the largest
+    finite value it rounds to infinity), as a Python float."""
+    if x == 0:
+        return 0.0
+    sign = -1.0 if x < 0 else 1.0
+    x = abs(x)
+    e = x.numerator.bit_length() - x.denominator.bit_length()
+    if Fraction(2) ** e > x:
+        e -= 1
+    ulp = Fraction(2) ** (max(e, -126) - 23)
+    q = x / ulp
+    whole = q.numerator // q.denominator
+    rest = q - whole
+    if rest > Fraction(1, 2) or (rest == Fraction(1, 2) and whole % 2):
+        whole += 1
+    v = whole * ulp
+    if v > F32_MAX:
+        return sign * math.inf
+    return sign * float(v)
+
+
+def silu_bf16(bits: int) -> int:
+    """bf16(silu(g)) of one bf16 value: the binary32 formula g / (1 + exp(-g)) of
+    h3_fused_ops.py:205 with each step correctly rounded -- e = RN(exp(-g)),
+    d = RN(1 + e), q = RN(g / d) -- then rounded to bf16.  exp(-g) is evaluated
+    to 60 digits and rounded once; every other step is exact rational
+    arithmetic rounded once.  Where exp(-g) overflows binary32 (g < -88.7) the
+    quotient is -0; +inf gives +inf, -inf and NaN give NaN."""
+    exponent, mantissa = (bits >> 7) & 0xFF, bits & 0x7F
+    if exponent == 0xFF:
+        if mantissa or bits & 0x8000:
+            return (bits | 0x0040) if mantissa else 0x7FC0
+        return bits
+    g = struct.unpack("<f", struct.pack("<I", bits << 16))[0]
+    if g == 0.0:
+        return bits
+    if -g > 89.0:
+        return 0x8000  # exp(-g) overflows: g / inf
+    if -g < -110.0:
+        e = 0.0  # exp(-g) < 2^-150 rounds to zero
+    else:
+        with localcontext() as ctx:
+            ctx.prec = 60
+            e = _f32_of_fraction(Fraction(Decimal(-g).exp()))
+        if math.isinf(e):
+            return 0x8000
+    d = _f32_of_fraction(1 + Fraction(e))
+    return _bf16_bits_of_double(_f32_of_fraction(Fraction(g) / Fraction(d)))
+
+
+# The silu window: bf16 magnitudes 2^-9 <= |g| < 2^7 (bit patterns 0x3B00 ..
+# 0x42FF without the sign), 2048 per sign.  Outside it the function is
+# bf16(g / 2) below, g above for g > 0 and g * 0 above for g < 0; the kernel
+# computes those and looks the window up (tests/test_silu_table.py checks the
+# whole rule against the oracle on every bf16 value).
+SILU_LO = 0x3B00
+SILU_N = 2048
+
+
+def silu_window_table() -> list[int]:
+    """binary32 bit patterns of bf16(silu(g)) over the window: entry i is the
+    pattern SILU_LO + i, entry SILU_N + i its negative."""
+    out = []
+    for sign in (0, 0x8000):
+        out.extend(silu_bf16(sign | (SILU_LO + i)) << 16 for i in range(SILU_N))
+    return out
+
+
+def write_silu_table() -> Path:
+    """csrc/_gen/silu_table.h: the window table of the SwiGLU epilogue."""
+    GENERATED.mkdir(exist_ok=True)
+    path = GENERATED / "silu_table.h"
+    table = silu_window_table()
+    rows = ["    " + ", ".join(f"0x{v:08x}u" for v in table[i:i + 8]) + "," for i in range(0, len(table), 8)]
+    text = (
+        "// Generated by vflash_amd/build.py (write_silu_table); not edited by hand.\n"
+        "// bf16(silu(g)) as binary32 bit patterns for 2^-9 <= |g| < 2^7: entry i is the bf16\n"
+        f"// pattern 0x{SILU_LO:04X} + i, entry {SILU_N} + i its negative.\n"
+        "#pragma once\n#include <stdint.h>\n\nnamespace vfa {\n\n"
+        f"constexpr uint32_t kSiluLo = 0x{SILU_LO:04X}u, kSiluN = {SILU_N}u;\n\n"
+        f"__device__ const uint32_t kSiluTable[{2 * SILU_N}] __attribute__((aligned(16))) = {{\n"
+        + "\n".join(rows)
+        + "\n};\n\n}  // namespace vfa\n"
+    )
+    if not path.exists() or path.read_text() != text:
+        path.write_text(text)
+    return path
+
+
 def write_activation_tables() -> Path:
     """csrc/_gen/activation_tables.h: the 65536-entry bf16 -> bf16 GELU-tanh table."""
     GENERATED.mkdir(exist_ok=True)
@@ -117,6 +212,7 @@ def build(verbose: bool = False) -> Path:
     """Compile every HIP source for gfx950 and link the C-ABI library."""
     OBJECTS.mkdir(exist_ok=True)
     write_activation_tables()
+    write_silu_table()
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError("no HIP sources found")

@@ -219,43 +219,6 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// silu(g) = g / (1 + exp(-g)) in binary32 for a bf16 value g, the formula of
-// the reference's SwiGLU kernel (h3_fused_ops.py:205) with each step close to
-// correctly rounded:
-//   exp(-g) = 2^t, t = -g log2(e).  log2(e) = L_HI + L_LO with L_HI of 16
-//     significant bits, so t_hi = -g L_HI is exact (g has at most 8); with
-//     n = rint(t_hi), a = (t_hi - n) + (-g L_LO) is the reduced argument to
-//     about 2^-26 (t_hi - n is exact), and e = 2^n * v_exp_f32(a) is within
-//     about one binary32 ulp of exp(-g) (Cody and Waite's additive range
-//     reduction; v_exp_f32 is accurate to one ulp on |a| <= 0.5).  t_hi is
-//     clamped to +-200, past which 2^t over- or underflows binary32 anyway.
-//   d = 1 + e, then q = g / d by Markstein's correction of the hardware
-//     reciprocal y: q0 = g y, r = g - q0 d (exact), q = q0 + r y, with the
-//     residual formed negated, r' = q0 d - g and q = q0 + r' (-y): the same
-//     value, and a zero quotient keeps the sign of g.  The hardware
-//     reciprocal flushes results below 2^-126 to zero, so where e >= 2^63
-//     (g <= -44) both g and d are scaled by 2^-64 first: d 2^-64 is formed as
-//     2^-64 + e 2^-64, which rounds exactly as 1 + e does, and g 2^-64 is exact.
-// Where r is NaN the quotient is a special case that q0 already holds:
-// g = +inf gives +inf, g = -inf or NaN gives NaN, and d = inf (exp(-g)
-// overflows for g <= -89) gives -0 -- the binary32 formula's own results.
-__device__ __forceinline__ float silu_of_bf16(float g) {
-  constexpr float L_HI = 1.44268798828125f;      // 47274 / 2^15
-  constexpr float L_LO = 7.0526075433008373e-06f;  // log2(e) - L_HI
-  const float th = __builtin_amdgcn_fmed3f(-g * L_HI, -200.0f, 200.0f);
-  const float n = __builtin_rintf(th);
-  const float a = __builtin_fmaf(-g, L_LO, th - n);
-  const float sc = n >= 63.0f ? 0x1p-64f : 1.0f;
-  const float e = __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f(a), (int)n) * sc;
-  const float d = sc + e;
-  const float gs = g * sc;
-  const float y = __builtin_amdgcn_rcpf(d);
-  const float q0 = gs * y;
-  const float r = __builtin_fmaf(q0, d, -gs);
-  const float q = __builtin_fmaf(r, -y, q0);
-  return r == r ? q : q0;
-}
-
 // E2M1 (OCP MX): bit 3 sign, bits 2..1 exponent (bias 1), bit 0 mantissa.
 // Codes 0..7 are 0, .5, 1, 1.5, 2, 3, 4, 6.  Built as binary32 bits directly.
 __device__ __forceinline__ float e2m1_to_f32(uint32_t c) {

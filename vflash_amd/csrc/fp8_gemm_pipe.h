@@ -280,7 +280,7 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
 template <int EPI, int BM, int BN, int NS, int PRE, bool SDMA>
 __global__ void __launch_bounds__(256, pipe_occupancy(BM, BN, NS)) fp8_gemm_pipe(const GemmParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t ring[pipe_lds(BM, BN, NS)];
-  __shared__ __attribute__((aligned(1024))) uint8_t vec[VEC_LDS];
+  __shared__ __attribute__((aligned(1024))) uint8_t vec[VEC_LDS + (EPI == EPI_SWIGLU ? SILU_LDS : 0)];
   int tm, tn;
   // SwiGLU tiles cover BN/2 value columns and their BN/2 gate columns.
   const int64_t tile_cols =

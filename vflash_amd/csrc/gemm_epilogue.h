@@ -1,6 +1,7 @@
 // Tile ordering and the two-phase epilogue shared by the GEMM kernels of this
 // path (E4M3 W8A8 and E2M1-weight W4A8).  Kernel-side only; not part of the C-ABI.
 #pragma once
+#include "_gen/silu_table.h"
 #include "common.h"
 #include "gemm_params.h"
 
@@ -87,6 +88,26 @@ __device__ __forceinline__ void lora_blocks(const GemmParams& p, int64_t m0, int
 // LDS bytes of the staged tile vectors: weight scales (or the one scalar),
 // activation row scales, bias.
 constexpr int VEC_LDS = 3 * 1024;
+// LDS bytes of the silu window table, which SwiGLU tiles stage after the vectors.
+constexpr int SILU_LDS = 2 * (int)kSiluN * 4;
+
+// bf16(silu(g)) as a binary32 value, for the bf16 pattern `bits` (low 16 bits)
+// of g: looked up in the window table `tab` (LDS) for 2^-9 <= |g| < 2^7, else
+// bf16(g / 2) below the window, g above it for g > 0 and g * 0 for g < 0 (-0,
+// or NaN for -inf and NaN).  Every bf16 input gives the binary32 formula
+// g / (1 + exp(-g)) of h3_fused_ops.py:205 with each step correctly rounded,
+// then rounded to bf16 (the window table is generated to that definition).
+__device__ __forceinline__ float silu_lookup(uint32_t bits, float g, const float* tab) {
+  const uint32_t a = bits & 0x7fffu;
+  const uint32_t i = a - kSiluLo;  // wraps around below the window
+  const uint32_t idx = min(i, kSiluN - 1u) | ((bits >> 4) & kSiluN);
+  const float t = tab[idx];
+  const float factor = a < kSiluLo ? 0.5f : ((bits & 0x8000u) ? 0.0f : 1.0f);
+  const float outside = g * factor;
+  // One rounding for both cases (table values are bf16 already), so that the
+  // choice stays a select rather than a branch around the conversion.
+  return round_bf16_wide(i < kSiluN ? t : outside);
+}
 
 // Copy the scale and bias vectors of a BM x BN tile into LDS (vec_lds) with
 // buffer-load-to-LDS DMA, one instruction each on waves 0, 1 and 2.  Issued
@@ -114,6 +135,14 @@ __device__ __forceinline__ void stage_vectors(const GemmParams& p, int64_t m0, i
       const uint32_t off = lane < 32 ? (uint32_t)(col * 2) : VFA_OOB;
       lds_dma16(make_rsrc(p.bias, (uint32_t)(p.n * 2)), vec_lds + 2048, off);
     }
+    // The silu window table after the vectors: SILU_LDS / 4 KB blocks of 1 KB per wave.
+    constexpr int BLOCKS = SILU_LDS / 4096;
+    static_assert(SILU_LDS % 4096 == 0, "four waves share the table's 1 KB blocks");
+    const __amdgpu_buffer_rsrc_t rt = make_rsrc(kSiluTable, (uint32_t)SILU_LDS);
+    static_for<BLOCKS>([&](auto j) {
+      const uint32_t blk = (uint32_t)(wave * BLOCKS + j);
+      lds_dma16(rt, vec_lds + VEC_LDS + blk * 1024u, blk * 1024u + (uint32_t)lane * 16u);
+    });
     return;
   }
   if (wave == 0) {
@@ -279,6 +308,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
     const int rows = (int)min((int64_t)BM, p.m - m0);
     const int parts = (int)((p.half_n + BN / 2 - 1) / (BN / 2));
     const int part = (int)(n0 / (BN / 2));
+    static_assert(VEC, "the silu table is staged with the vectors");
+    const float* const silu_tab = reinterpret_cast<const float*>(vec + VEC_LDS);
     // The swizzle of row r0 + it * RPO repeats every two passes: two LDS
     // offsets per half serve every pass.  The chunks of a batch of rows are
     // read before any is used, so the LDS latency is paid once per batch.
@@ -314,9 +345,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const uint32_t vw = (uint32_t)vv[j][q], gw = (uint32_t)gg[j][q];
-          const float g0 = bf16_lo(gw), g1 = bf16_hi(gw);
-          const uint32_t sp = pack_bf16x2(silu_of_bf16(g0), silu_of_bf16(g1));
-          const uint32_t hw = pack_bf16x2(bf16_lo(vw) * bf16_lo(sp), bf16_hi(vw) * bf16_hi(sp));
+          const float s0 = silu_lookup(gw, bf16_lo(gw), silu_tab);
+          const float s1 = silu_lookup(gw >> 16, bf16_hi(gw), silu_tab);
+          const uint32_t hw = pack_bf16x2(bf16_lo(vw) * s0, bf16_hi(vw) * s1);
           amax_pk = abs_max_pk(amax_pk, hw);
           h[q] = (int)hw;
         }
