@@ -175,9 +175,12 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
   // Block scales of the current 16-K block as binary16 pairs: steps 2b and
   // 2b + 1 of a half share block b, so each is converted once per two steps.
   v2h scw[NB], sca[A4 ? MB : 1];
-  // MFMA step v (0..3) of a half held in r.
-  auto step = [&](const Raw& r, auto v) {
+  // Binary16 operands of MFMA step v (0..3) of a half held in r.
+  struct Ops {
     v8h xa[MB], xw[NB];
+  };
+  auto convert = [&](const Raw& r, auto v) {
+    Ops o;
     // E4M3 block scale (byte 2*fh + v/2 of the row's scale word), exact in binary16.
     auto scale_pair = [&](uint32_t sword) {
       const uint32_t sb = (sword >> (16 * fh + 8 * (v / 2))) & 0xffu;
@@ -197,7 +200,7 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
     };
     static_for<MB>([&](auto mb) {
       if constexpr (A4) {
-        xa[mb] = fp4x8((uint32_t)r.a[mb][0][(int)v], sca[mb]);
+        o.xa[mb] = fp4x8((uint32_t)r.a[mb][0][(int)v], sca[mb]);
       } else {
         const uint32_t d0 = (uint32_t)r.a[mb][v / 2][(v % 2) * 2];
         const uint32_t d1 = (uint32_t)r.a[mb][v / 2][(v % 2) * 2 + 1];
@@ -205,15 +208,29 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
         const v2h x1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, true);
         const v2h x2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, false);
         const v2h x3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, true);
-        xa[mb] = v8h{x0[0], x0[1], x1[0], x1[1], x2[0], x2[1], x3[0], x3[1]};
+        o.xa[mb] = v8h{x0[0], x0[1], x1[0], x1[1], x2[0], x2[1], x3[0], x3[1]};
       }
     });
-    static_for<NB>([&](auto nb) { xw[nb] = fp4x8((uint32_t)r.w[nb][(int)v], scw[nb]); });
+    static_for<NB>([&](auto nb) { o.xw[nb] = fp4x8((uint32_t)r.w[nb][(int)v], scw[nb]); });
+    return o;
+  };
+  // The MFMAs of one step, with the dequantization of the next step (nxt, from
+  // half r, step v) interleaved: one MFMA, then three VALU instructions (four
+  // with E2M1 activations, whose dequantization is longer), so the VALU work
+  // runs while the MFMA pipe is busy instead of between its bursts.
+  auto pipelined = [&](const Ops& cur, const Raw& r, auto v) {
+    const Ops nxt = convert(r, v);
     static_for<NB>([&](auto nb) {
       static_for<MB>([&](auto mb) {
-        acc[nb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xw[nb], xa[mb], acc[nb][mb], 0, 0, 0);
+        acc[nb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.xw[nb], cur.xa[mb], acc[nb][mb], 0, 0, 0);
       });
     });
+    static_for<NB * MB>([&](auto) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, A4 ? 4 : 3, 0);
+    });
+    __builtin_amdgcn_sched_barrier(0);
+    return nxt;
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
@@ -230,16 +247,16 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
   read_raw(r0, 0, I0{});
   // Same pending LDS reads on both loop entries (see the W8A8 kernel).
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  // Software pipeline: cur holds the converted operands of the next MFMA step.
+  Ops cur = convert(r0, I0{});
   for (int kt = 0; kt < KT; ++kt) {
     const int j = kt & 1;
     read_raw(r1, j, I1{});
-    step(r0, I0{});
-    step(r0, I1{});
-    step(r0, I2{});
-    step(r0, I3{});
-    step(r1, I0{});
-    step(r1, I1{});
-    __builtin_amdgcn_sched_barrier(0);
+    cur = pipelined(cur, r0, I1{});
+    cur = pipelined(cur, r0, I2{});
+    cur = pipelined(cur, r0, I3{});
+    cur = pipelined(cur, r1, I0{});
+    cur = pipelined(cur, r1, I1{});
     // Stage kt+1 has landed for every wave and stage kt is fully read.
     wait_vmcnt<0, true>();
     asm volatile("" ::: "memory");
@@ -247,8 +264,10 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
     asm volatile("" ::: "memory");
     issue(j, kt + 2);
     read_raw(r0, 1 - j, I0{});
-    step(r1, I2{});
-    step(r1, I3{});
+    cur = pipelined(cur, r1, I2{});
+    cur = pipelined(cur, r1, I3{});
+    // Half 0 of stage kt+1 (zeros past the last stage, never multiplied).
+    cur = pipelined(cur, r0, I0{});
   }
   wait_vmcnt<0, true>();  // every DMA has landed before the ring becomes the staging tile
   __builtin_amdgcn_s_barrier();
