@@ -199,14 +199,29 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
   // columns per g for this lane) are live while its MB row blocks are written.
   // Two copies (with and without bias) keep the bias test out of the loop.
   auto phase1 = [&](auto has_bias) {
+    // Every column block's LDS vector reads come first.  As far as the
+    // compiler knows the staging writes below may alias them, so a read placed
+    // after a write waits for that write, and reads issued block by block would
+    // each pay a full LDS round trip.
+    v4f s4r[VEC ? NB : 1][4];
+    uint2 b4r[VEC ? NB : 1][4];
+    if constexpr (VEC) {
+      static_for<NB>([&](auto nb) {
+        static_for<4>([&](auto g) {
+          const int col = wn * WN + nb * 32 + g * 8 + fh * 4;
+          s4r[nb][g] = *reinterpret_cast<const v4f*>(vec + col * 4);
+          b4r[nb][g] = has_bias ? *reinterpret_cast<const uint2*>(vec + 2048 + col * 2)
+                                : make_uint2(0u, 0u);
+        });
+      });
+    }
     static_for<NB>([&](auto nb) {
       float sv[4][4], bv[4][4];
       static_for<4>([&](auto g) {
         const int col = wn * WN + nb * 32 + g * 8 + fh * 4;  // tile column of value i = 0
         if constexpr (VEC) {
-          const v4f s4 = *reinterpret_cast<const v4f*>(vec + col * 4);
-          uint2 b4 = make_uint2(0u, 0u);
-          if constexpr (has_bias) b4 = *reinterpret_cast<const uint2*>(vec + 2048 + col * 2);
+          const v4f s4 = s4r[nb][g];
+          const uint2 b4 = b4r[nb][g];
           static_for<4>([&](auto i) {
             sv[g][i] = sw_vector ? s4[(int)i] : sw0;
             const uint32_t bw = i < 2 ? b4.x : b4.y;
