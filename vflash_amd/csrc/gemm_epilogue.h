@@ -279,11 +279,11 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
         }
         static_for<4>([&](auto g) {
           uint32_t w[2];
-          // Output pairs: every bf16 rounding is one v_cvt_pk_bf16_f32 for two values.
+          // Output pairs: a bf16 rounding whose result is used again is one
+          // conversion per value (round_bf16_wide); the last one is one
+          // v_cvt_pk_bf16_f32 for the pair.
           static_for<2>([&](auto h) {
             constexpr int i0 = 2 * h, i1 = 2 * h + 1;
-            // A rounding whose result is used again is one conversion per value
-            // (round_bf16_wide), the last one per pair.
             float y0 = acc[nb][mb][g * 4 + i0] * sam[mb] * sv[g][i0];
             float y1 = acc[nb][mb][g * 4 + i1] * sam[mb] * sv[g][i1];
             if constexpr (has_bias) {
