@@ -312,6 +312,34 @@ def test_silu_epilogue_on_every_bf16_gate_value(dev):
     assert int(differ.sum()) == 0
 
 
+def test_silu_epilogue_on_non_finite_and_extreme_gates(dev):
+    # The closed forms outside the silu table's window: +inf stays +inf, -inf
+    # and NaN give NaN, the largest negative bf16 gives -0, bf16 subnormals give
+    # bf16(g / 2); the window's edges on both sides.  Same construction as above:
+    # zero operands make each gate column its bias.
+    gates = np.array([np.inf, -np.inf, np.nan, 3.3895314e38, -3.3895314e38, 128.0, -128.0,
+                      127.5, -127.5, 2.0**-9, -(2.0**-9), 2.0**-10, -(2.0**-10), 1e-40, -1e-40,
+                      -88.0, -89.0, -100.0], np.float32)
+    gates = bf16_round(gates)
+    f = 128
+    gate_cols = np.zeros(f, np.float32)
+    gate_cols[: gates.size] = gates
+    bias = torch.from_numpy(np.concatenate([np.ones(f, np.float32), gate_cols])).to(torch.bfloat16)
+    m, k = 16, 64
+    a = torch.zeros((m, k), dtype=torch.float8_e4m3fn, device=dev)
+    sa = torch.ones((m, 1), dtype=torch.float32, device=dev)
+    w = torch.zeros((2 * f, k), dtype=torch.float8_e4m3fn, device=dev)
+    sw = torch.ones((2 * f, 1), dtype=torch.float32, device=dev)
+    h, _ = kernels.fp8_gemm_swiglu(a, sa, w, sw, m, bias.to(dev))
+    got = h.float().cpu().numpy()[0, : gates.size]
+    want = O.silu(gates)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    assert np.array_equal(got[fin].view(np.uint32), want[fin].view(np.uint32))
+    assert got[0] == np.inf and np.isnan(got[1]) and np.isnan(got[2])
+    assert got[4] == 0.0 and np.signbit(got[4])
+
+
 
 def test_portable_mode_keeps_torchs_scalar_division_on_the_gpu(dev):
     # One row per positive finite bf16 maximum.  The portable ("torch") mode is
