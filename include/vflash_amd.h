@@ -112,8 +112,8 @@ int vflash_gelu_quantize_rows_e4m3(const void* y, int64_t m, int64_t k, int64_t 
  * [F, 2F) the gate columns of the packed output, as .chunk(2, dim=-1) splits it.
  *   p   = bf16(bf16(acc * sa * sw) + bias)            (the packed [m, 2F] output)
  *   h   = bf16(p[:, f] * bf16(silu(p[:, F + f])))     written to h [m, F] (ldh), with
- *         silu(x) = x / (1 + exp(-x)) evaluated in binary32 with an exponential
- *         and a quotient each within about one ulp of correctly rounded
+ *         silu(x) = x / (1 + exp(-x)) in binary32 with each step correctly
+ *         rounded (the exponential, the sum and the quotient), then rounded to bf16
  *   amax_part fp32 [m, vflash_swiglu_parts(n)]: max |h| of each row over each
  *   128-column group, consumed by vflash_requant_rows_e4m3.
  *   Requires n % 256 == 0, ldh % 8 == 0, h and sw (and bias) 16-byte aligned.
@@ -123,8 +123,44 @@ int vflash_fp8_linear_swiglu(const void* a, const float* sa, int64_t lda, const 
                              const void* bias, void* h, int64_t ldh, float* amax_part,
                              void* stream);
 
+/*
+ * vflash_fp8_linear_swiglu with the FFN input adapter merged into the packed
+ * projection before the activation (t, lora_b NULL: no adapter, the plain entry).
+ * Replaces triton_strict_bf16_ffn_adapter_silu and its eager twin
+ *   (src/vflash/native/h3_fused_ops.py:229-286, 703-763;
+ *   src/vflash/native/h3_native_denoiser.py:318-325, 375-382, 1081-1101):
+ *   p'  = bf16(p + delta) for value and gate columns alike, with
+ *         delta = bf16(t . B^T), then bf16(delta * scale) if scale != 1 and
+ *         bf16(delta * strength) if strength != 1 (the adapter chain of
+ *         vflash_fp8_linear_lora)
+ *   h   = bf16(p'[:, f] * bf16(silu(p'[:, F + f]))), amax_part as in
+ *         vflash_fp8_linear_swiglu.
+ *   t bf16 [m, >= rank] (ldt);  lora_b bf16 [n, >= rank] (ldb): value rows, then
+ *   gate rows, of the adapter's up-projection;  1 <= rank <= 128; ldt, ldb
+ *   multiples of 8; t, lora_b 16-byte aligned.
+ */
+int vflash_fp8_linear_swiglu_lora(const void* a, const float* sa, int64_t lda, const void* w,
+                                  const float* sw, int64_t ldw, int64_t m, int64_t n, int64_t k,
+                                  const void* bias, const void* t, int64_t ldt,
+                                  const void* lora_b, int64_t ldb, int64_t rank, float scale,
+                                  float strength, void* h, int64_t ldh, float* amax_part,
+                                  void* stream);
+
 /* Number of 128-column groups per row in the SwiGLU amax_part: ceil(n / 2 / 128). */
 int64_t vflash_swiglu_parts(int64_t n);
+
+/*
+ * The tiling vflash_fp8_linear and the other E4M3 GEMM entries use for an
+ * m x n output on a device with `compute_units` CUs (a host-side query; no
+ * device work).  0: 256x256, 1: 256x192, 2: 256x128, 3: 128x192, 4: 128x128
+ * (two workgroups per CU), 5: 128x128 (one per CU, grids of one round),
+ * 6: 128x64, 7: 64x64.  The SwiGLU entries always use 256x256.  No tiling
+ * changes a result bit; this exists so that tests can aim shapes at each one.
+ * branch_cols > 0 (a multiple of 32): the choice of a LoRA entry with adapter
+ * branches that wide, which takes only tilings whose wave width (half the tile
+ * width) divides branch_cols.
+ */
+int vflash_fp8_gemm_tiling(int64_t m, int64_t n, int64_t compute_units, int64_t branch_cols);
 
 /*
  * vflash_fp8_linear_swiglu followed by vflash_requant_rows_e4m3 in one call
@@ -212,17 +248,40 @@ int vflash_fp8_linear_gate_residual(const void* a, const float* sa, int64_t lda,
                                     void* stream);
 
 /*
+ * vflash_fp8_linear_gate_residual with an adapter merged before the gate: the
+ * adapted gate-residual of the attention output and FFN down projections.
+ * Replaces _adapted_gate_residual and triton_strict_bf16_adapter_gate_residual
+ *   (src/vflash/native/h3_native_denoiser.py:327-338, 551, 570, 1271-1290;
+ *   src/vflash/native/h3_fused_ops.py:341-418, 982-1028):
+ *   y'  = bf16(y + delta), delta as in vflash_fp8_linear_lora
+ *   out = bf16(residual + bf16(gate * y'))
+ *   t, lora_b NULL: no adapter (vflash_fp8_linear_gate_residual).  The adapter
+ *   operands follow vflash_fp8_linear_lora; the gate and residual
+ *   vflash_fp8_linear_gate_residual.
+ */
+int vflash_fp8_linear_lora_gate_residual(
+    const void* a, const float* sa, int64_t lda, const void* w, const float* sw, int64_t ldw,
+    int64_t m, int64_t n, int64_t k, const void* bias, const void* gate, int64_t gate_ts,
+    int64_t gate_hs, int64_t gate_tokens, const int64_t* gate_index, int64_t gate_rows,
+    const void* residual, int64_t ldr, const void* t, int64_t ldt, const void* lora_b,
+    int64_t ldb, int64_t rank, float scale, float strength, void* out, int64_t ldo,
+    void* stream);
+
+/*
  * LoRA down-projection t = bf16(x . A^T) (binary32 accumulation).
  * Replaces the inner F.linear of the activation-adapter hook
  *   (src/vflash/adapters/h3_reference_lora.py:80-82).
- *   x bf16 [m, k] (ldx);  lora_a bf16 [rank, k] contiguous;  t bf16 [m, rank] contiguous
- *   Requires rank % 16 == 0, rank <= 128, k % 16 == 0, ldx % 8 == 0.
+ *   x bf16 [m, k] (ldx);  lora_a bf16 [rank, k] contiguous;  t bf16 [m, ldt]:
+ *   columns [0, rank) hold t, columns [rank, ceil16(rank)) are written as zeros.
+ *   Requires 1 <= rank <= 512 (three stacked Q/K/V adapters of rank 128 fit),
+ *   ldt >= ceil16(rank), ldt % 8 == 0, k % 16 == 0, ldx % 8 == 0; x, lora_a, t
+ *   16-byte aligned.
  * Sum order: K is cut into 8 chunks of 32-element steps, [S c / 8, S (c + 1) / 8)
  * with S = ceil(k / 32), each accumulated from zero; t = bf16 of the chunk
- * sums added in chunk order.  The order depends on k only, never on m.
+ * sums added in chunk order.  The order depends on k only, never on m or rank.
  */
 int vflash_lora_down(const void* x, int64_t m, int64_t k, int64_t ldx, const void* lora_a,
-                     int64_t rank, void* t, void* stream);
+                     int64_t rank, void* t, int64_t ldt, void* stream);
 
 /*
  * Per-token E4M3 quantization and the LoRA down-projection of the same rows in
@@ -231,12 +290,13 @@ int vflash_lora_down(const void* x, int64_t m, int64_t k, int64_t ldx, const voi
  * (src/vflash/native/h3_fp8_activation.py:12-55) plus the adapter hook's inner
  * F.linear (src/vflash/adapters/h3_reference_lora.py:80-82) for the adapter
  * linears.
- *   Requires k % 16 == 0, rank % 16 == 0, 16 <= rank <= 128, ldx % 8 == 0,
- *   m_pad >= m; x, lora_a 16-byte aligned; codes, t 8-byte aligned.
+ *   Requires k % 16 == 0, ldx % 8 == 0, m_pad >= m, the rank and t layout of
+ *   vflash_lora_down; x, lora_a, t 16-byte aligned; codes 8-byte aligned.
  */
 int vflash_quantize_rows_lora_e4m3(const void* x, int64_t m, int64_t k, int64_t ldx,
                                    void* codes, float* scales, int64_t m_pad,
-                                   const void* lora_a, int64_t rank, void* t, void* stream);
+                                   const void* lora_a, int64_t rank, void* t, int64_t ldt,
+                                   void* stream);
 
 /*
  * W8A8 linear with a fused LoRA up-projection and merge.
@@ -246,13 +306,41 @@ int vflash_quantize_rows_lora_e4m3(const void* x, int64_t m, int64_t k, int64_t 
  *   delta = bf16(t . B^T); if scale != 1: bf16(delta * scale);
  *           if strength != 1: bf16(delta * strength)
  *   out   = bf16(base + delta)
- *   t bf16 [m, rank] (ldt);  lora_b bf16 [n, rank] (ldb);  rank % 16 == 0, <= 128.
+ *   t bf16 [m, >= rank] (ldt);  lora_b bf16 [n, >= rank] (ldb);  1 <= rank <= 128;
+ *   ldt, ldb multiples of 8 (reads stop at the rank rounded up to 8; positions
+ *   at or past the rank count as zero); t, lora_b 16-byte aligned.
  */
 int vflash_fp8_linear_lora(const void* a, const float* sa, int64_t lda, const void* w,
                            const float* sw, int64_t ldw, int64_t m, int64_t n, int64_t k,
                            const void* bias, const void* t, int64_t ldt, const void* lora_b,
                            int64_t ldb, int64_t rank, float scale, float strength, void* out,
                            int64_t ldo, void* stream);
+
+/*
+ * vflash_fp8_linear_lora with up to three adapter branches, each with its own
+ * scale, over equal runs of output columns: the Q/K/V adapters of a merged
+ * projection.  Replaces the QKV residual pack and its merges
+ *   (src/vflash/native/h3_native_denoiser.py:301-316, 1153-1194;
+ *   src/vflash/native/h3_fused_ops.py:297-340, 802-838, 900-980):
+ *   column c belongs to branch b = c / (n / branches);
+ *   delta = bf16(t[:, b * t_branch .. + rank] . B^T) then bf16(delta * scales[b])
+ *           if scales[b] != 1 and bf16(delta * strength) if strength != 1;
+ *   out  = bf16(base + delta), written as one matrix (plane_cols 0, ldo) or
+ *          into planes as vflash_fp8_linear_planes (plane_cols, plane_stride).
+ *   lora_b bf16 [n, >= rank]: branch b's up-projection rows stacked in column
+ *   order; a branch of smaller rank has zero columns up to `rank`.
+ *   scales: host array of `branches` floats (read before the call returns).
+ *   Requires 1 <= branches <= 3, n % branches == 0, (n / branches) % 32 == 0
+ *   when branches > 1, t_branch >= rank and a multiple of 8, ldt >=
+ *   (branches - 1) * t_branch + rank, and the operand rules of vflash_fp8_linear_lora.
+ */
+int vflash_fp8_linear_lora_branches(const void* a, const float* sa, int64_t lda, const void* w,
+                                    const float* sw, int64_t ldw, int64_t m, int64_t n,
+                                    int64_t k, const void* bias, const void* t, int64_t ldt,
+                                    int64_t t_branch, const void* lora_b, int64_t ldb,
+                                    int64_t rank, int64_t branches, const float* scales,
+                                    float strength, void* out, int64_t ldo, int64_t plane_cols,
+                                    int64_t plane_stride, void* stream);
 
 /*
  * NVFP4-weight linear (W4A8: E4M3 per-token activations, E2M1 weights with

@@ -191,15 +191,47 @@ def lora_merge(base, delta) -> np.ndarray:
     return bf16_round(np.asarray(base, F32) + np.asarray(delta, F32))
 
 
+def adapted(base, x, adapter, strength: float = 1.0) -> np.ndarray:
+    """A projection with a low-rank residual merged in, bf16(base + delta) with
+    delta = lora_delta(x, down, up, scaling): the native block's _adapted_linear
+    (src/vflash/native/h3_native_denoiser.py:280-299, 318-325) and its fused
+    merges (h3_fused_ops.py:297-340, 765-800), which round the scaled delta and
+    the sum the same way.  ``adapter`` is (down [r, K], up [N, r], scaling) or
+    None (the base unchanged)."""
+    if adapter is None:
+        return np.asarray(base, F32)
+    down, up, scaling = adapter
+    return lora_merge(base, lora_delta(x, down, up, scaling, strength))
+
+
+def qkv_adapted(base, x, adapters) -> np.ndarray:
+    """The merged QKV projection with its Q/K/V residual pack: third b of the
+    output takes adapter b (h3_native_denoiser.py:301-316; the fused merges
+    h3_fused_ops.py:802-838, 954-980 round each branch the same way)."""
+    base = np.asarray(base, F32)
+    third = base.shape[1] // 3
+    return np.concatenate(
+        [adapted(base[:, b * third : (b + 1) * third], x, adapters[b]) for b in range(3)], axis=1
+    )
+
+
+def adapted_gate_residual(residual, gate, base, x, adapter) -> np.ndarray:
+    """bf16(residual + bf16(gate * bf16(base + delta))): _adapted_gate_residual
+    (h3_native_denoiser.py:327-338) and strict_adapter_gate_residual_kernel
+    (h3_fused_ops.py:341-418)."""
+    return gate_residual(residual, gate, adapted(base, x, adapter))
+
+
 def ffn(x, up_codes, up_scale, up_bias, down_codes, down_scale, down_bias, gate, residual,
-        activation: str = "gelu_tanh"):
-    """The FFN chain of this path: up + bias, activation (GELU-tanh, or the H3
-    SwiGLU on a packed [2F, H] up projection), per-token requant, down + bias,
-    gate-residual.  Returns (g, h_codes, h_scales, out)."""
+        activation: str = "gelu_tanh", up_adapter=None, down_adapter=None):
+    """The FFN chain of this path: up + bias (+ the input adapter), activation
+    (GELU-tanh, or the H3 SwiGLU on a packed [2F, H] up projection), per-token
+    requant, down + bias (+ the output adapter on the activation), gate-residual
+    (h3_native_denoiser.py:375-382, 563-576).  Returns (g, h_codes, h_scales, out)."""
     x = np.asarray(x, F32)
     m = x.shape[0]
-    up = w8a8_linear(x, up_codes, up_scale, up_bias)
+    up = adapted(w8a8_linear(x, up_codes, up_scale, up_bias), x, up_adapter)
     g = silu_mul(up) if activation == "swiglu" else gelu_tanh(up)
     h_codes, h_scales = quantize_rows(g)
     y = add_bias(scaled_mm(h_codes[:m], h_scales[:m], down_codes, down_scale), down_bias)
-    return g, h_codes, h_scales, gate_residual(residual, gate, y)
+    return g, h_codes, h_scales, gate_residual(residual, gate, adapted(y, g, down_adapter))

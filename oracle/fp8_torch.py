@@ -128,3 +128,29 @@ def gate_residual(residual, gate, y) -> torch.Tensor:
     """fp8.gate_residual: bf16(residual + bf16(gate * y)) in binary32."""
     gated = bf16_round(gate.float() * y.float())
     return bf16_round(residual.float() + gated)
+
+
+def lora_delta(x, lora_a, lora_b, scaling: float = 1.0, strength: float = 1.0) -> torch.Tensor:
+    """fp8.lora_delta: t = bf16(x A^T); d = bf16(t B^T) (binary64 sums);
+    bf16(d * scaling) if scaling != 1 and bf16(d * strength) if strength != 1,
+    each product formed in binary32."""
+    t = bf16_round(x.double() @ lora_a.double().T)
+    d = bf16_round(t.double() @ lora_b.double().T)
+    for f in (scaling, strength):
+        if f != 1.0:
+            d = bf16_round(d * torch.tensor(f, dtype=torch.float32, device=d.device))
+    return d
+
+
+def lora_merge(base, delta) -> torch.Tensor:
+    """fp8.lora_merge: bf16(base + delta), the sum formed in binary32."""
+    return bf16_round(base.float() + delta.float())
+
+
+def adapted(base, x, adapter, strength: float = 1.0) -> torch.Tensor:
+    """fp8.adapted: bf16(base + lora_delta(x, down, up, scaling)); base when
+    ``adapter`` (down, up, scaling) is None."""
+    if adapter is None:
+        return base.float()
+    down, up, scaling = adapter
+    return lora_merge(base, lora_delta(x, down, up, scaling, strength))

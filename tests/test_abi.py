@@ -31,6 +31,9 @@ def test_header_declares_the_path():
         "vflash_fp8_linear_gate_residual",
         "vflash_lora_down",
         "vflash_fp8_linear_lora",
+        "vflash_fp8_linear_lora_branches",
+        "vflash_fp8_linear_lora_gate_residual",
+        "vflash_fp8_linear_swiglu_lora",
         "vflash_nvfp4_linear",
     ):
         assert must in names
@@ -45,7 +48,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_status_strings_and_version():
     lib = _lib.library()
-    assert lib.vflash_abi_version() == 3
+    assert lib.vflash_abi_version() == _lib.ABI_VERSION == 4
     assert lib.vflash_status_string(_lib.VFLASH_EINVAL) == b"argument outside the declared contract"
     assert lib.vflash_swiglu_parts(28672) == 112 and lib.vflash_swiglu_parts(256) == 1
 
@@ -72,8 +75,68 @@ def test_nvfp4_and_lora_contracts():
     p = ctypes.c_void_p(256)
     # n not a multiple of 128
     assert lib.vflash_nvfp4_linear(p, p, 64, p, p, p, 1, 64, 64, None, p, 64, None) == -1
-    # rank not a multiple of 16
-    assert lib.vflash_lora_down(p, 4, 64, 64, p, 20, p, None) == -1
+    # rank 0 or past 512, and a t row stride below ceil16(rank) or not a multiple of 8
+    assert lib.vflash_lora_down(p, 4, 64, 64, p, 0, p, 16, None) == -1
+    assert lib.vflash_lora_down(p, 4, 64, 64, p, 513, p, 528, None) == -1
+    assert lib.vflash_lora_down(p, 4, 64, 64, p, 20, p, 24, None) == -1
+    assert lib.vflash_lora_down(p, 4, 64, 64, p, 20, p, 36, None) == -1
+    assert lib.vflash_quantize_rows_lora_e4m3(p, 4, 64, 64, p, p, 16, p, 20, p, 24, None) == -1
+
+
+def _gemm_head(p):
+    return [p, p, 64, p, p, 64, 16, 96, 64, None]
+
+
+def test_adapter_entry_contracts():
+    lib = _lib.library()
+    p = ctypes.c_void_p(256)
+    one = (ctypes.c_float * 3)(1.0, 1.0, 1.0)
+    # rank 0 and 129; ldb not a multiple of 8; ldt below the rank
+    for rank, ldt, ldb in ((0, 16, 16), (129, 136, 136), (16, 16, 20), (16, 8, 16)):
+        assert lib.vflash_fp8_linear_lora(*_gemm_head(p), p, ldt, p, ldb, rank, 1.0, 1.0, p, 96,
+                                          None) == -1
+    # branches: 4 branches, a branch width that is not a multiple of 32 (n 96 / 3 = 32 is one),
+    # t_branch below the rank, ldt too short for the last branch
+    assert lib.vflash_fp8_linear_lora_branches(*_gemm_head(p), p, 64, 16, p, 16, 16, 4, one, 1.0,
+                                               p, 96, 0, 0, None) == -1
+    head = _gemm_head(p)
+    head[7] = 144  # n 144: branches of 48 columns
+    assert lib.vflash_fp8_linear_lora_branches(*head, p, 64, 16, p, 16, 16, 3, one, 1.0, p, 144,
+                                               0, 0, None) == -1
+    assert lib.vflash_fp8_linear_lora_branches(*_gemm_head(p), p, 64, 8, p, 16, 16, 3, one, 1.0,
+                                               p, 96, 0, 0, None) == -1
+    assert lib.vflash_fp8_linear_lora_branches(*_gemm_head(p), p, 40, 16, p, 16, 16, 3, one, 1.0,
+                                               p, 96, 0, 0, None) == -1
+    # no scales array; overlapping planes
+    assert lib.vflash_fp8_linear_lora_branches(*_gemm_head(p), p, 48, 16, p, 16, 16, 3, None, 1.0,
+                                               p, 96, 0, 0, None) == -1
+    assert lib.vflash_fp8_linear_lora_branches(*_gemm_head(p), p, 48, 16, p, 16, 16, 3, one, 1.0,
+                                               p, 32, 32, 32, None) == -1
+    # gate-residual with an adapter of rank 0; SwiGLU with n % 256
+    assert lib.vflash_fp8_linear_lora_gate_residual(
+        *_gemm_head(p), p, 96, 1, 16, None, 0, p, 96, p, 16, p, 16, 0, 1.0, 1.0, p, 96, None) == -1
+    head = _gemm_head(p)
+    head[7] = 384
+    assert lib.vflash_fp8_linear_swiglu_lora(*head, p, 16, p, 16, 16, 1.0, 1.0, p, 192, p,
+                                             None) == -1
+
+
+def test_tiling_query_routes_shapes():
+    # Host-side query of the GEMM tiling (no device work): the automatic choice,
+    # and branch widths that exclude the 192-column tilings (96-column waves).
+    lib = _lib.library()
+    names = ("256x256", "256x192", "256x128", "128x192", "128x128", "128x128 one round", "128x64",
+             "64x64")
+    pick = lambda m, n, b=0: names[lib.vflash_fp8_gemm_tiling(m, n, 256, b)]
+    assert pick(32760, 13824) == "256x256"
+    assert pick(4096, 3072) == "256x192"
+    assert pick(2100, 3712) == "128x128"
+    assert pick(520, 4112) == "128x128 one round"
+    assert pick(257, 528) == "64x64"
+    assert pick(4096, 3072, 1024) != "256x192"
+    assert 5120 % (int(pick(32760, 15360, 5120).split("x")[1].split()[0]) // 2) == 0
+    assert lib.vflash_fp8_gemm_tiling(16, 16, 256, 48) == -1  # branch width not a multiple of 32
+    assert lib.vflash_fp8_gemm_tiling(0, 16, 256, 0) == -1
 
 
 def test_gate_residual_and_producer_contracts():
@@ -84,6 +147,9 @@ def test_gate_residual_and_producer_contracts():
                                                None, 0, p, 64, p, 64, None) == -1
     assert lib.vflash_fp8_linear_gate_residual(p, p, 64, p, p, 64, 16, 64, 64, None, p, 64, 1, 16,
                                                p, 0, p, 64, p, 64, None) == -1
+    # out aliasing the residual with another row stride
+    assert lib.vflash_fp8_linear_gate_residual(p, p, 64, p, p, 64, 16, 64, 64, None, p, 64, 1, 16,
+                                               None, 0, p, 64, p, 128, None) == -1
     # k not a multiple of 8, a NaN eps, a misaligned modulation row stride
     args = [p, 4, 12, 16, None, 1e-6, p, 16, p, 16, 4, None, 0, None, 0, p, p, 16, None]
     assert lib.vflash_rmsnorm_modulate_quantize_e4m3(*args) == -1

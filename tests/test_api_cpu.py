@@ -286,3 +286,53 @@ def test_bench_operand_variants_keep_the_shapes_and_finite_codes():
     qc, qs = O.quantize_rows(rx.float().numpy())
     assert np.all(qs[:48] == 1.0)
     assert np.array_equal(qc[:48], rx.float().to(torch.float8_e4m3fn).view(torch.uint8).numpy())
+
+
+def test_stacked_qkv_adapters_layout():
+    # stack_adapters lays the Q/K/V pack out for one down-projection and one
+    # epilogue: branch b's down rows at b * R (R = ceil16 of the largest rank),
+    # its up rows in its third of the columns, zeros elsewhere.
+    from vflash_amd.fused import LowRankResidual, stack_adapters
+
+    g = torch.Generator().manual_seed(0)
+    k, inner = 64, 32
+    ranks = (16, 8, 20)
+    res = [LowRankResidual(torch.randn((r, k), generator=g).to(torch.bfloat16),
+                           torch.randn((inner, r), generator=g).to(torch.bfloat16), s)
+           for r, s in zip(ranks, (0.5, 1.0, 0.0625))]
+    st = stack_adapters(res, k, 3 * inner)
+    assert st.rank == 20 and st.width == 32 and st.scalings == (0.5, 1.0, 0.0625)
+    assert st.down.shape == (96, k) and st.up.shape == (96, 20)
+    assert st.up.stride(0) % 8 == 0  # rows padded to whole 8-element groups
+    for b, r in enumerate(res):
+        rank = r.down.shape[0]
+        assert torch.equal(st.down[b * 32 : b * 32 + rank], r.down)
+        assert not st.down[b * 32 + rank : (b + 1) * 32].any()
+        assert torch.equal(st.up[b * inner : (b + 1) * inner, :rank], r.up)
+        assert not st.up[b * inner : (b + 1) * inner, rank:].any()
+
+
+def test_low_rank_residual_refusals():
+    from vflash_amd.fused import LowRankResidual, stack_adapters
+
+    k, inner = 64, 32
+    ok = LowRankResidual(torch.zeros((16, k), dtype=torch.bfloat16),
+                         torch.zeros((inner, 16), dtype=torch.bfloat16), 1.0)
+    with pytest.raises(ValueError, match="three branches"):
+        stack_adapters([ok] * 4, k, 3 * inner)
+    with pytest.raises(ValueError, match="does not match"):
+        stack_adapters([ok] * 3, k + 16, 3 * inner)
+    bad_rank = LowRankResidual(torch.zeros((16, k), dtype=torch.bfloat16),
+                               torch.zeros((inner, 8), dtype=torch.bfloat16), 1.0)
+    with pytest.raises(ValueError, match="compatible"):
+        stack_adapters([ok, ok, bad_rank], k, 3 * inner)
+    fp32 = LowRankResidual(torch.zeros((16, k)), torch.zeros((inner, 16)), 1.0)
+    with pytest.raises(ValueError, match="BF16"):
+        stack_adapters([ok, ok, fp32], k, 3 * inner)
+    inf = LowRankResidual(ok.down, ok.up, float("inf"))
+    with pytest.raises(ValueError, match="finite"):
+        stack_adapters([ok, ok, inf], k, 3 * inner)
+    big = LowRankResidual(torch.zeros((136, k), dtype=torch.bfloat16),
+                          torch.zeros((inner, 136), dtype=torch.bfloat16), 1.0)
+    with pytest.raises(ValueError, match="ranks up to 128"):
+        stack_adapters([ok, ok, big], k, 3 * inner)

@@ -14,34 +14,10 @@ pytestmark = pytest.mark.gpu
 
 
 
-# The tilings of csrc/fp8_gemm.hip (kTilings): tile rows, tile columns,
-# relative throughput per output, and whether the tiling only runs where the
-# grid fits one round.
-TILINGS = {
-    "256x256": (256, 256, 1.00, False),
-    "256x192": (256, 192, 0.95, False),
-    "256x128": (256, 128, 0.90, False),
-    "128x192": (128, 192, 0.85, False),
-    "128x128": (128, 128, 0.80, False),
-    "128x128 one round": (128, 128, 0.85, True),
-    "128x64": (128, 64, 0.60, False),
-    "64x64": (64, 64, 0.50, False),
-}
-
-
-def tiling(m, n, cus=256):
-    """The GEMM tiling the library picks for an M x N output on `cus` compute
-    units (csrc/fp8_gemm.hip, pick_tiling): the least ceil(tiles / CUs) x tile
-    outputs / throughput, the larger tile first on ties."""
-    best = None
-    for name, (bm, bn, rate, one_round) in TILINGS.items():
-        tiles = -(-m // bm) * -(-n // bn)
-        if one_round and tiles > cus:
-            continue
-        cost = -(-tiles // cus) * bm * bn / rate
-        if best is None or cost < best[0]:
-            best = (cost, name)
-    return best[1]
+def tiling(m, n):
+    """The GEMM tiling the library picks for an M x N output on 256 CUs (the
+    library's own rule, vflash_fp8_gemm_tiling)."""
+    return kernels.gemm_tiling(m, n)
 
 
 # Edge shapes under each tiling: partial row and column tiles, K tails
@@ -51,7 +27,7 @@ EDGES = [
     (257, 256, 528, "64x64"),
     (257, 144, 4112, "128x64"), (300, 256, 4112, "128x64"),
     (520, 144, 4112, "128x128 one round"), (300, 256, 7184, "128x128 one round"),
-    (1040, 144, 13840, "128x128"), (2100, 256, 7184, "128x128"),
+    (600, 144, 11008, "128x128"), (2100, 256, 3712, "128x128"),
     (257, 144, 13840, "128x192"), (700, 256, 6032, "128x192"),
     (1040, 48, 6160, "256x128"), (1100, 256, 6032, "256x128"),
     (1040, 144, 7184, "256x192"), (1100, 256, 8208, "256x192"),

@@ -46,10 +46,10 @@ def inputs(m, k, n, seed=0):
 # tiles take the scalar-offset DMA and partial ones the vector-offset form.
 #   4096 x 3088, 4100 x 3088, 4100 x 3072: 256x256 (16 or 4 weight rows, 4
 #   activation rows in the last tiles); 1100 x 8208: 256x192; 1040 x 6160:
-#   256x128; 700 x 6032: 128x192; 2100 x 7184: 128x128, two per CU;
+#   256x128; 700 x 6032: 128x192; 2100 x 3712: 128x128, two per CU;
 #   520 x 4112: 128x128 in one round; 300 x 4112: 128x64; 257 x 528: 64x64.
 @pytest.mark.parametrize("m,n", [(4096, 3088), (4100, 3088), (4100, 3072), (1100, 8208),
-                                 (1040, 6160), (700, 6032), (2100, 7184), (520, 4112),
+                                 (1040, 6160), (700, 6032), (2100, 3712), (520, 4112),
                                  (300, 4112), (257, 528)])
 def test_linear_tail_tiles_match_untailed_operands(dev, m, n):
     k = 384

@@ -310,3 +310,76 @@ def test_modulate_oracle_is_torch_eager_bf16():
     # Leaving out the bf16 rounding of 1 + scale is visible.
     fused = bf16_round(bf16_round(n.float().numpy() * (1.0 + scale.float().numpy())) + shift.float().numpy())
     assert (fused != ref).sum() > 0
+
+
+def _exact_adapter_case(rng, m, k, n, rank):
+    """Integer-valued operands whose sums are exact in binary32, so torch's CPU
+    bf16 matmuls (binary32 accumulation, one rounding) round the exact sums, as
+    the oracle does: t takes values up to k * 9, beyond bf16's 8-bit significand,
+    so its rounding is exercised; base values are random bf16."""
+    x = rng.integers(-3, 4, (m, k)).astype(np.float32)
+    down = rng.integers(-3, 4, (rank, k)).astype(np.float32)
+    up = rng.integers(-3, 4, (n, rank)).astype(np.float32)
+    base = bf16_round(rng.standard_normal((m, n)).astype(np.float32) * 300)
+    return x, down, up, base
+
+
+def _bf(a):
+    return torch.from_numpy(np.asarray(a, np.float32)).to(torch.bfloat16)
+
+
+def test_adapted_chains_are_the_reference_eager_expressions():
+    # The native block's adapter paths written as the reference writes them
+    # (h3_native_denoiser.py:280-338: F.linear(F.linear(x, down), up) * scaling,
+    # base + that, residual + gate * projected) and evaluated by torch in bf16
+    # on the CPU, against the oracle's adapted / adapted_gate_residual chains.
+    import torch.nn.functional as F
+
+    rng = np.random.default_rng(11)
+    m, k, n, rank = 48, 64, 96, 16
+    x, down, up, base = _exact_adapter_case(rng, m, k, n, rank)
+    residual = bf16_round(rng.standard_normal((m, n)).astype(np.float32) * 100)
+    gate = bf16_round(rng.random(n).astype(np.float32))
+    for scaling in (1.0, 0.0625, 0.3, 1.375):
+        ref = _bf(base) + F.linear(F.linear(_bf(x), _bf(down)), _bf(up)) * scaling
+        got = O.adapted(base, x, (down, up, scaling))
+        assert np.array_equal(got.view(np.uint32), ref.float().numpy().view(np.uint32))
+        ref_g = _bf(residual) + _bf(gate) * ref
+        got_g = O.adapted_gate_residual(residual, gate, base, x, (down, up, scaling))
+        assert np.array_equal(got_g.view(np.uint32), ref_g.float().numpy().view(np.uint32))
+    # A chain that skips the rounding of the scaled delta differs.
+    d = O.lora_delta(x, down, up)
+    wrong = bf16_round(base + d * np.float32(0.3))
+    assert not np.array_equal(wrong, O.adapted(base, x, (down, up, 0.3)))
+
+
+def test_qkv_and_ffn_input_adapters_are_the_reference_eager_expressions():
+    # _qkv_linear: torch.cat(chunk_b + _residual_linear(x, residual_b)) with three
+    # branches of their own rank and scaling (h3_native_denoiser.py:301-316), and
+    # _ffn_input: _silu_mul(_adapted_linear(...)) (:375-382).
+    import torch.nn.functional as F
+
+    rng = np.random.default_rng(12)
+    m, k, inner = 40, 64, 32
+    x = rng.integers(-3, 4, (m, k)).astype(np.float32)
+    base = bf16_round(rng.standard_normal((m, 3 * inner)).astype(np.float32) * 300)
+    adapters = []
+    for rank, scaling in ((16, 0.0625), (8, 0.3), (24, 1.0)):
+        adapters.append((rng.integers(-3, 4, (rank, k)).astype(np.float32),
+                         rng.integers(-3, 4, (inner, rank)).astype(np.float32), scaling))
+    chunks = _bf(base).chunk(3, dim=-1)
+    ref = torch.cat([c + F.linear(F.linear(_bf(x), _bf(a)), _bf(b)) * s
+                     for c, (a, b, s) in zip(chunks, adapters)], dim=-1)
+    got = O.qkv_adapted(base, x, adapters)
+    assert np.array_equal(got.view(np.uint32), ref.float().numpy().view(np.uint32))
+    # The branches are not interchangeable: swapping two changes the result.
+    swapped = O.qkv_adapted(base, x, [adapters[1], adapters[0], adapters[2]])
+    assert not np.array_equal(swapped, got)
+
+    down = rng.integers(-3, 4, (16, k)).astype(np.float32)
+    up = rng.integers(-3, 4, (2 * inner, 16)).astype(np.float32)
+    packed = _bf(base[:, : 2 * inner] / 64) + F.linear(F.linear(_bf(x), _bf(down)), _bf(up)) * 0.0625
+    value, g = packed.chunk(2, dim=-1)
+    ref = value * F.silu(g)
+    got = O.silu_mul(O.adapted(bf16_round(base[:, : 2 * inner] / 64), x, (down, up, 0.0625)))
+    assert np.array_equal(got.view(np.uint32), ref.float().numpy().view(np.uint32))

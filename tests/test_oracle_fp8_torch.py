@@ -81,3 +81,18 @@ def test_activations_are_the_oracles_activations():
     want = O.silu_mul(y.float().numpy())
     same = got.view(np.uint32) == want.view(np.uint32)
     assert np.all(same | (np.isnan(got) & np.isnan(want)))
+
+
+def test_adapter_chain_is_the_oracles_chain():
+    rng = np.random.default_rng(4)
+    m, k, n, rank = 33, 320, 72, 24
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(torch.bfloat16)
+    down = torch.from_numpy(rng.standard_normal((rank, k)).astype(np.float32) * 0.05).to(torch.bfloat16)
+    up = torch.from_numpy(rng.standard_normal((n, rank)).astype(np.float32) * 0.05).to(torch.bfloat16)
+    base = torch.from_numpy(rng.standard_normal((m, n)).astype(np.float32)).to(torch.bfloat16)
+    for scaling, strength in ((1.0, 1.0), (0.0625, 1.0), (0.3, 1.375)):
+        got = T.adapted(base, x, (down, up, scaling), strength).numpy()
+        want = O.adapted(base.float().numpy(), x.float().numpy(),
+                         (down.float().numpy(), up.float().numpy(), scaling), strength)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert torch.equal(T.adapted(base, x, None), base.float())

@@ -20,6 +20,7 @@ VFLASH_EINVAL = -1
 VFLASH_ELAUNCH = -2
 VFLASH_ESCRATCH = -3
 NOALLOC_SCRATCH_BYTES = 16 << 20
+ABI_VERSION = 4
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -57,13 +58,30 @@ SIGNATURES: dict[str, tuple[list, object]] = {
          _P, _I64, _P],
         _I32,
     ),
-    "vflash_lora_down": ([_P, _I64, _I64, _I64, _P, _I64, _P, _P], _I32),
-    "vflash_quantize_rows_lora_e4m3": ([_P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P, _P], _I32),
+    "vflash_fp8_linear_lora_gate_residual": (
+        [_P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _I64, _P, _I64,
+         _P, _I64, _P, _I64, _I64, _F32, _F32, _P, _I64, _P],
+        _I32,
+    ),
+    "vflash_lora_down": ([_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P], _I32),
+    "vflash_quantize_rows_lora_e4m3": (
+        [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P, _I64, _P], _I32),
     "vflash_fp8_linear_lora": (
         [_P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _I64, _F32, _F32,
          _P, _I64, _P],
         _I32,
     ),
+    "vflash_fp8_linear_lora_branches": (
+        [_P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _I64, _I64,
+         ctypes.POINTER(_F32), _F32, _P, _I64, _I64, _I64, _P],
+        _I32,
+    ),
+    "vflash_fp8_linear_swiglu_lora": (
+        [_P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _I64, _F32, _F32,
+         _P, _I64, _P, _P],
+        _I32,
+    ),
+    "vflash_fp8_gemm_tiling": ([_I64, _I64, _I64, _I64], _I32),
     "vflash_nvfp4_linear": (
         [_P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _P],
         _I32,
@@ -91,7 +109,7 @@ def library() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = restype
-    if lib.vflash_abi_version() != 3:
+    if lib.vflash_abi_version() != ABI_VERSION:
         raise RuntimeError("libvflash_amd.so has an unexpected ABI version")
     return lib
 

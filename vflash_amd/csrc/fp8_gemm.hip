@@ -17,6 +17,13 @@
 //   EPI_SWIGLU h = bf16(value * bf16(silu(gate))) with value = base[:, f] and
 //              gate = base[:, half_n + f], plus per-row |h| maxima per 128
 //              columns (h3_native_denoiser.py:369-376, h3_fused_ops.py:184-224)
+//   EPI_LORA_GATE   EPI_GATE on bf16(base + delta): the adapted gate-residual
+//              (h3_native_denoiser.py:327-338, h3_fused_ops.py:341-418)
+//   EPI_SWIGLU_LORA EPI_SWIGLU on bf16(base + delta) for value and gate columns
+//              alike (h3_fused_ops.py:229-286, strict_ffn_adapter_silu_kernel)
+// The LoRA delta may come from up to three adapter branches with their own
+// scales, each owning a contiguous run of output columns (the Q/K/V adapters of
+// a merged projection, h3_native_denoiser.py:301-316, h3_fused_ops.py:900-980).
 #include "fp8_gemm_pipe.h"
 
 namespace vfa {
@@ -24,6 +31,7 @@ namespace vfa {
 extern template hipError_t launch_tiling<EPI_BIAS>(const GemmParams&, int, hipStream_t);
 extern template hipError_t launch_tiling<EPI_GATE>(const GemmParams&, int, hipStream_t);
 extern template hipError_t launch_tiling<EPI_LORA>(const GemmParams&, int, hipStream_t);
+extern template hipError_t launch_tiling<EPI_LORA_GATE>(const GemmParams&, int, hipStream_t);
 
 // Compute units of the current device (cached per device id).
 int compute_units() {
@@ -61,21 +69,27 @@ constexpr Tiling kTilings[GEMM_TILINGS] = {
     {128, 64, 0.60, false},  {64, 64, 0.50, false},
 };
 
-int pick_tiling(const GemmParams& p) {
-  const int64_t cus = compute_units();
+// branch_cols > 0 (a LoRA epilogue with several adapter branches of that many
+// columns): only tilings whose wave width (BN / 2) divides branch_cols, so that
+// each wave's columns belong to one branch.  The 128x64 and 64x64 tilings
+// (32-column waves) serve every multiple of 32.
+int pick_tiling(int64_t m, int64_t n, int64_t cus, int64_t branch_cols) {
+  auto allowed = [&](int t) { return branch_cols <= 0 || branch_cols % (kTilings[t].bn / 2) == 0; };
   // Grids of three or more rounds of 256x256 tiles are MFMA-bound, and there
   // the largest tile's operand reuse wins: at 4095 x 5120 x 13824 it takes
   // 0.246 ms against 0.251 for 256x192, 0.265 for 256x128 and 0.272-0.274 for
   // the 128-row tiles (whose throughputs below come from one-round grids).
-  if (((p.m + 255) / 256) * ((p.n + 255) / 256) >= 3 * cus) return GEMM_256x256;
-  int best = GEMM_256x256;
+  if (((m + 255) / 256) * ((n + 255) / 256) >= 3 * cus && allowed(GEMM_256x256))
+    return GEMM_256x256;
+  int best = -1;
   double best_cost = 0.0;
   for (int t = 0; t < GEMM_TILINGS; ++t) {
     const Tiling& c = kTilings[t];
-    const int64_t tiles = ((p.m + c.bm - 1) / c.bm) * ((p.n + c.bn - 1) / c.bn);
+    if (!allowed(t)) continue;
+    const int64_t tiles = ((m + c.bm - 1) / c.bm) * ((n + c.bn - 1) / c.bn);
     if (c.one_round_only && tiles > cus) continue;
     const double cost = (double)((tiles + cus - 1) / cus) * c.bm * c.bn / c.rate;
-    if (t == 0 || cost < best_cost) {
+    if (best < 0 || cost < best_cost) {
       best = t;
       best_cost = cost;
     }
@@ -98,17 +112,21 @@ int tiling_group_m(int tiling, int64_t tile_cols) {
 // GemmParams::group_m is set here from the tiling.
 hipError_t launch_fp8_gemm(const GemmParams& params, int epi, hipStream_t s) {
   GemmParams p = params;
-  if (epi == EPI_SWIGLU) {
+  if (epi_swiglu(epi)) {
     // One tiling: 128 value + 128 gate columns, the 256x256 schedule.
     p.group_m = tiling_group_m(GEMM_256x256, (p.half_n + 127) / 128);
+    if (epi == EPI_SWIGLU_LORA) return launch_pipe<EPI_SWIGLU_LORA, PipeCfg<256, 256, 2, 0>>(p, s);
     return launch_pipe<EPI_SWIGLU, PipeCfg<256, 256, 2, 0>>(p, s);
   }
-  const int tiling = pick_tiling(p);
+  const int tiling =
+      pick_tiling(p.m, p.n, compute_units(), epi_lora(epi) ? p.lora_branch_cols : 0);
+  if (tiling < 0) return hipErrorInvalidValue;
   p.group_m = tiling_group_m(tiling, (p.n + kTilings[tiling].bn - 1) / kTilings[tiling].bn);
   switch (epi) {
     case EPI_BIAS: return launch_tiling<EPI_BIAS>(p, tiling, s);
     case EPI_GATE: return launch_tiling<EPI_GATE>(p, tiling, s);
     case EPI_LORA: return launch_tiling<EPI_LORA>(p, tiling, s);
+    case EPI_LORA_GATE: return launch_tiling<EPI_LORA_GATE>(p, tiling, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -60,7 +60,7 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
   static_assert(DMA_A % 2 == 0 && DMA_W % 2 == 0,
                 "blocks alternate between the two swizzle parities");
 
-  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * (EPI == EPI_SWIGLU ? BN / 2 : BN);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * (epi_swiglu(EPI) ? BN / 2 : BN);
   // The lane index comes from mbcnt and the wave index arrives as a scalar.
   const int lane = (int)__builtin_amdgcn_mbcnt_hi(-1, __builtin_amdgcn_mbcnt_lo(-1, 0));
   const int tid_v = wave * 64 + lane;
@@ -75,7 +75,7 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
   // past the operand's end.  Partial tiles keep every row step in the lane
   // offset, where the range check turns rows past the end into zeros.
   bool full = rows_a == BM;
-  if constexpr (EPI == EPI_SWIGLU) {
+  if constexpr (epi_swiglu(EPI)) {
     // Waves 0-1 load tile rows 0..BN/2-1 = value rows n0.., waves 2-3 load tile
     // rows BN/2.. = gate rows half_n + n0.. (the resource is based BN/2 rows
     // earlier, so tile row r maps to half_n + n0 + r - BN/2).
@@ -202,12 +202,12 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
   // before the K loop (up to 128 registers held through it), so the epilogue
   // does not wait on their loads; the 256x192 and 256x256 tiles, whose
   // registers hold the main loop, compute them in the epilogue.
-  constexpr bool LORA_PRE = EPI == EPI_LORA && MB * NB <= 8;
+  constexpr bool LORA_PRE = epi_lora(EPI) && MB * NB <= 8;
   v16f lora_d[LORA_PRE ? MB * NB : 1];
-  if constexpr (LORA_PRE) lora_blocks<BM, BN, WGM, WGN>(p, m0, n0, wm, wn, lane, lora_d);
+  if constexpr (LORA_PRE) lora_blocks<BM, BN, WGM, WGN, epi_swiglu(EPI)>(p, m0, n0, wm, wn, lane, lora_d);
   // Prologue and K loop; use_sdma selects the scalar-offset DMA (full tiles).
   auto main_loop = [&](auto use_sdma) {
-    stage_vectors<BM, BN, EPI == EPI_SWIGLU>(p, m0, n0, wave, lane, vec_lds);
+    stage_vectors<BM, BN, epi_swiglu(EPI)>(p, m0, n0, wave, lane, vec_lds);
     static_for<NS>([&](auto s) { issue((int)s, (int)s, use_sdma); });
     wait_vmcnt<(NS - 1) * DMA, true>();
     __builtin_amdgcn_s_barrier();
@@ -280,11 +280,11 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
 template <int EPI, int BM, int BN, int NS, int PRE, bool SDMA>
 __global__ void __launch_bounds__(256, pipe_occupancy(BM, BN, NS)) fp8_gemm_pipe(const GemmParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t ring[pipe_lds(BM, BN, NS)];
-  __shared__ __attribute__((aligned(1024))) uint8_t vec[VEC_LDS + (EPI == EPI_SWIGLU ? SILU_LDS : 0)];
+  __shared__ __attribute__((aligned(1024))) uint8_t vec[VEC_LDS + (epi_swiglu(EPI) ? SILU_LDS : 0)];
   int tm, tn;
   // SwiGLU tiles cover BN/2 value columns and their BN/2 gate columns.
   const int64_t tile_cols =
-      EPI == EPI_SWIGLU ? (p.half_n + BN / 2 - 1) / (BN / 2) : (p.n + BN - 1) / BN;
+      epi_swiglu(EPI) ? (p.half_n + BN / 2 - 1) / (BN / 2) : (p.n + BN - 1) / BN;
   tile_coords((int)((p.m + BM - 1) / BM), (int)tile_cols, p.group_m, tm, tn);
   pipe_tile<EPI, BM, BN, NS, PRE, SDMA>(p, tm, tn, ring,
                                         __builtin_amdgcn_readfirstlane(lds_addr(ring)), vec,
@@ -302,7 +302,7 @@ struct PipeCfg {
 template <int EPI, class C>
 static hipError_t launch_pipe(const GemmParams& p, hipStream_t s) {
   const int64_t tile_cols =
-      EPI == EPI_SWIGLU ? (p.half_n + C::BN / 2 - 1) / (C::BN / 2) : (p.n + C::BN - 1) / C::BN;
+      epi_swiglu(EPI) ? (p.half_n + C::BN / 2 - 1) / (C::BN / 2) : (p.n + C::BN - 1) / C::BN;
   const dim3 grid((unsigned)(((p.m + C::BM - 1) / C::BM) * tile_cols));
   if (p.k % 128)
     fp8_gemm_pipe<EPI, C::BM, C::BN, C::NS, C::PRE, false><<<grid, dim3(256), 0, s>>>(p);

@@ -33,42 +33,73 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group_
   grouped_tile(x * q + min(x, r) + i, tiles_m, tiles_n, group_m, tm, tn);
 }
 
-// Epilogue shared by every tiling, in two phases through LDS.
-//
-// Phase 1 (per wave, from the accumulators): a lane holds, for 32x32 block
-// (nb, mb) and register r, tile row mb*32 + (lane & 31) and tile column
-// nb*32 + 8*(r/4) + 4*(lane/32) + r%4 of its wave's sub-tile.  It applies the
-// scales, bias and the register-level epilogue (LoRA merge), rounds to
-// bf16 and writes the values into a BM x BN bf16 staging tile in LDS (16-byte
-// chunk c of row r stored in slot c ^ (r % chunks-per-row)).  Scale and bias
-// vectors are loaded once, before any store.
-// Phase 2 (whole workgroup): each thread moves 16-byte row chunks from LDS to
-// global memory with coalesced 16-byte stores, applying the gate-residual
-// epilogue there with coalesced residual loads.
+// Adapter operands of the LoRA epilogues.  A rank step covers 16 rank
+// positions; lane half fh supplies positions 16 st + 8 fh .. +7 of its row.
+// Positions at or past the rank read as zero, so a rank that is not a multiple
+// of 16 needs no padding of t or B.  A row is read only below the rank rounded
+// up to 8, which the row strides (ldt, ldb >= that, multiples of 8) contain.
+__device__ __forceinline__ v8s lora_frag(const uint16_t* row, int rank, int st, int fh, bool ok) {
+  const int e0 = st * 16 + fh * 8;
+  v8s v = (ok && e0 < rank) ? *reinterpret_cast<const v8s*>(row + e0) : v8s{};
+  if (rank & 7) {  // uniform: only ranks that end inside an 8-element vector
+    const int valid = rank - e0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (e >= valid) v[e] = 0;
+  }
+  return v;
+}
+
+// Global column (row of the adapter's B) of tile column c.  SwiGLU tiles hold
+// value columns n0 .. in [0, BN/2) and the matching gate columns half_n + n0 ..
+// in [BN/2, BN), as the GEMM tile maps them.
+template <int BN, bool SWIGLU>
+__device__ __forceinline__ int64_t tile_column(const GemmParams& p, int64_t n0, int c) {
+  if constexpr (SWIGLU) return c < BN / 2 ? n0 + c : p.half_n + n0 + c - BN / 2;
+  return n0 + c;
+}
+
+// The adapter branch of a wave's columns, from its first column `col`: the
+// offset of its t columns and its scale.  A wave's columns lie in one branch
+// (the launcher picks a tiling whose wave width divides lora_branch_cols).
+struct LoraBranch {
+  int64_t toff;
+  float scale;
+};
+__device__ __forceinline__ LoraBranch lora_branch(const GemmParams& p, int64_t col) {
+  // At most three branches: two comparisons instead of a 64-bit division.
+  const int64_t bc = p.lora_branch_cols;
+  const int b = bc > 0 && col < p.n ? (int)(col >= bc) + (int)(col >= 2 * bc) : 0;
+  // The three scales pass through readfirstlane before the choice: a choice
+  // between plain loads of them would be folded into one indexed load of the
+  // kernel's parameter block, which then gets copied to private memory.
+  auto arg = [](float v) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v))); };
+  const float s0 = arg(p.lora_scale[0]), s1 = arg(p.lora_scale[1]), s2 = arg(p.lora_scale[2]);
+  const float s = b == 0 ? s0 : (b == 1 ? s1 : s2);
+  return LoraBranch{b * p.lora_t_branch, s};
+}
+
 // LoRA products of one wave's blocks, d[nb * MB + mb] = B[n, :] . t[m, :]
 // (bf16 MFMA, binary32 accumulation), with all loads issued before the MFMAs.
 // Computed ahead of the main loop so the epilogue does not wait on them.
-template <int BM, int BN, int WGM, int WGN>
+template <int BM, int BN, int WGM, int WGN, bool SWIGLU = false>
 __device__ __forceinline__ void lora_blocks(const GemmParams& p, int64_t m0, int64_t n0, int wm,
                                             int wn, int lane, v16f* d) {
   constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
   constexpr int RS = 8;  // rank steps of 16: rank <= 128
   const int fr = lane & 31, fh = lane >> 5;
+  const LoraBranch br = lora_branch(p, tile_column<BN, SWIGLU>(p, n0, wn * WN));
   v8s bf[NB][RS], tf[MB][RS];
   static_for<NB>([&](auto nb) {
-    const int64_t nrow = n0 + wn * WN + nb * 32 + fr;
+    const int64_t nrow = tile_column<BN, SWIGLU>(p, n0, wn * WN + nb * 32) + fr;
     static_for<RS>([&](auto r) {
-      bf[nb][r] = (r * 16 < p.rank && nrow < p.n)
-                      ? *reinterpret_cast<const v8s*>(p.lora_b + nrow * p.ldb + r * 16 + fh * 8)
-                      : v8s{};
+      bf[nb][r] = lora_frag(p.lora_b + nrow * p.ldb, p.rank, r, fh, nrow < p.n);
     });
   });
   static_for<MB>([&](auto mb) {
     const int64_t m = m0 + wm * WM + mb * 32 + fr;
     static_for<RS>([&](auto r) {
-      tf[mb][r] = (r * 16 < p.rank && m < p.m)
-                      ? *reinterpret_cast<const v8s*>(p.lora_t + m * p.ldt + r * 16 + fh * 8)
-                      : v8s{};
+      tf[mb][r] = lora_frag(p.lora_t + m * p.ldt + br.toff, p.rank, r, fh, m < p.m);
     });
   });
   static_for<NB>([&](auto nb) {
@@ -157,10 +188,23 @@ __device__ __forceinline__ void stage_vectors(const GemmParams& p, int64_t m0, i
   }
 }
 
+// Epilogue shared by every tiling, in two phases through LDS.
+//
+// Phase 1 (per wave, from the accumulators): a lane holds, for 32x32 block
+// (nb, mb) and register r, tile row mb*32 + (lane & 31) and tile column
+// nb*32 + 8*(r/4) + 4*(lane/32) + r%4 of its wave's sub-tile.  It applies the
+// scales, bias and the register-level epilogue (LoRA merge), rounds to
+// bf16 and writes the values into a BM x BN bf16 staging tile in LDS (16-byte
+// chunk c of row r stored in slot c ^ (r % chunks-per-row)).  Scale and bias
+// vectors are loaded once, before any store.
+// Phase 2 (whole workgroup): each thread moves 16-byte row chunks from LDS to
+// global memory with coalesced 16-byte stores, applying the gate-residual
+// epilogue there with coalesced residual loads.
+//
 // VEC: read the scale and bias vectors from the LDS copy `vec` made by
 // stage_vectors (true), or from global memory (false).
-// lora_d: for EPI_LORA, the per-block LoRA products computed ahead of the main
-// loop ([nb * MB + mb], same layout as acc), or null to compute them here.
+// lora_d: for the LoRA epilogues, the per-block LoRA products computed ahead of
+// the main loop ([nb * MB + mb], same layout as acc), or null to compute them here.
 template <int BM, int BN, int WGM, int WGN, int EPI, bool VEC = false>
 __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
                                               v16f (&acc)[BN / WGN / 32][BM / WGM / 32],
@@ -176,6 +220,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
   static_assert(CH % SWZ == 0 && (SWZ & (SWZ - 1)) == 0, "swizzle stays inside the row");
   constexpr int PITCH = BN * 2;
   const int lane = tid & 63, fr = lane & 31, fh = lane >> 5;
+  constexpr bool LORA = epi_lora(EPI), GATE = epi_gate(EPI), SWIGLU = epi_swiglu(EPI);
+  const LoraBranch br =
+      LORA ? lora_branch(p, tile_column<BN, SWIGLU>(p, n0, wn * WN)) : LoraBranch{0, 1.0f};
   const float* __restrict__ sa_p = p.sa;
   const float* __restrict__ sw_p = p.sw;
   const uint16_t* __restrict__ bias_p = p.bias;
@@ -241,23 +288,18 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
         const int64_t m = m0 + row;
         const bool mvalid = m < p.m;
         v16f d = v16f{};
-        if (EPI == EPI_LORA && lora_d) {
+        if (LORA && lora_d) {
           d = lora_d[nb * MB + mb];
-        } else if constexpr (EPI == EPI_LORA) {
+        } else if constexpr (LORA) {
           // delta block = B[n, :] . t[m, :] on bf16 MFMA, binary32 accumulate.  The
           // operands of every rank step (rank <= 128) are loaded before the first
           // MFMA, so a block waits for one memory round trip, not one per step.
-          const int64_t nrow = n0 + wn * WN + nb * 32 + fr;
+          const int64_t nrow = tile_column<BN, SWIGLU>(p, n0, wn * WN + nb * 32) + fr;
           const bool nok = nrow < p.n;
           v8s bfr[8], tfr[8];
           static_for<8>([&](auto st) {
-            const bool live = st * 16 < p.rank;
-            bfr[st] = (live && nok) ? *reinterpret_cast<const v8s*>(p.lora_b + nrow * p.ldb +
-                                                                   st * 16 + fh * 8)
-                                    : v8s{};
-            tfr[st] = (live && mvalid) ? *reinterpret_cast<const v8s*>(p.lora_t + m * p.ldt +
-                                                                      st * 16 + fh * 8)
-                                       : v8s{};
+            bfr[st] = lora_frag(p.lora_b + nrow * p.ldb, p.rank, st, fh, nok);
+            tfr[st] = lora_frag(p.lora_t + m * p.ldt + br.toff, p.rank, st, fh, mvalid);
           });
           static_for<8>([&](auto st) {
             if (st * 16 < p.rank)
@@ -266,7 +308,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
                                                           0, 0);
           });
         }
-        if constexpr (EPI == EPI_LORA) {
+        if constexpr (LORA) {
           // delta = bf16(t . B^T), then the optional bf16(delta * scale) and
           // bf16(delta * strength) steps, for the block's 16 values at once (two
           // uniform branches per block); d then holds bf16 values as binary32.
@@ -274,7 +316,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
             static_for<16>([&](auto i) { d[(int)i] = round_bf16_wide(d[(int)i] * f); });
           };
           round_pairs(1.0f);
-          if (p.lora_scale != 1.0f) round_pairs(p.lora_scale);
+          if (br.scale != 1.0f) round_pairs(br.scale);
           if (p.lora_strength != 1.0f) round_pairs(p.lora_strength);
         }
         static_for<4>([&](auto g) {
@@ -290,7 +332,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
               y0 = round_bf16_wide(y0) + bv[g][i0];
               y1 = round_bf16_wide(y1) + bv[g][i1];
             }
-            if constexpr (EPI == EPI_LORA) {
+            if constexpr (LORA) {
               y0 = round_bf16_wide(y0) + d[g * 4 + i0];
               y1 = round_bf16_wide(y1) + d[g * 4 + i1];
             }
@@ -310,7 +352,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
 
   __syncthreads();
 
-  if constexpr (EPI == EPI_SWIGLU) {
+  if constexpr (SWIGLU) {
     // Phase 2 of the SwiGLU tile: value chunk c and gate chunk c + CH/2 of a
     // row give 8 outputs h = bf16(value * bf16(silu(gate))) (the eager bf16
     // order of h3_fused_ops.py:184-224); the 16 threads of a row also reduce
@@ -400,7 +442,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
   auto lds_chunk = [&](int row) {
     return *reinterpret_cast<const v4i*>(stage + row * PITCH + ((c ^ (row & (SWZ - 1))) << 4));
   };
-  // EPI_GATE: the residual chunk and the gate chunk of output row m0 + row,
+  // Gate-residual epilogues: the residual chunk and the gate chunk of output row m0 + row,
   // whose gate row is that of token `tok` (m % gate_tokens), through the index
   // when one is given (the adaLN gather read in place).  An index outside
   // [0, gate_rows) makes the row's gate NaN (quiet-NaN bf16 pairs in place of
@@ -409,7 +451,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
   struct GateIn {
     v4i res, gate;
   };
-  const bool vec_in = EPI == EPI_GATE && p.gate_hs == 1 &&
+  const bool vec_in = GATE && p.gate_hs == 1 &&
                       ((reinterpret_cast<uintptr_t>(p.gate) | reinterpret_cast<uintptr_t>(p.residual)) & 15) == 0 &&
                       p.gate_ts % 8 == 0 && p.ldr % 8 == 0;
   auto gate_in = [&](int row, int64_t tok, auto vec) {
@@ -459,17 +501,17 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
       reinterpret_cast<uint2*>(dst)[1] = make_uint2((uint32_t)v[2], (uint32_t)v[3]);
     }
   };
-  // Token of row r0 (EPI_GATE), advanced by RPP rows per pass.
-  const int64_t tokens = EPI == EPI_GATE ? p.gate_tokens : 1;
-  int64_t tok = EPI == EPI_GATE ? (m0 + r0) % tokens : 0;
-  const int64_t tok_step = EPI == EPI_GATE ? RPP % tokens : 0;
+  // Token of row r0 (gate-residual epilogues), advanced by RPP rows per pass.
+  const int64_t tokens = GATE ? p.gate_tokens : 1;
+  int64_t tok = GATE ? (m0 + r0) % tokens : 0;
+  const int64_t tok_step = GATE ? RPP % tokens : 0;
   auto next_tok = [&]() {
     tok += tok_step;
     if (tok >= tokens) tok -= tokens;
   };
   auto pass = [&](auto vec_out) {
-    if (rows == BM && (EPI != EPI_GATE || vec_in)) {
-      // A whole tile (with vector residual and gate loads for EPI_GATE): the
+    if (rows == BM && (!GATE || vec_in)) {
+      // A whole tile (with vector residual and gate loads for the gate-residual): the
       // chunks of BATCH rows (and their residual and gate chunks) are loaded
       // before any is stored, so each latency is paid once
       // per batch, not once per row.  The swizzle of row r0 + it * RPP repeats
@@ -492,7 +534,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
           const int it = it0 + j;
           const int row = r0 + it * RPP;
           v[j] = *reinterpret_cast<const v4i*>(stage + lofs[it & 3] + it * RPP * PITCH);
-          if constexpr (EPI == EPI_GATE) {
+          if constexpr (GATE) {
             if (it < PASSES && (PASSES * RPP == BM || row < BM))
               in[j] = gate_in(row, tok, std::true_type{});
             next_tok();
@@ -504,7 +546,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
           const int row = r0 + it * RPP;
           if (it < PASSES && (PASSES * RPP == BM || row < BM)) {
             v4i o = v[j];
-            if constexpr (EPI == EPI_GATE) o = gate_apply(o, in[j]);
+            if constexpr (GATE) o = gate_apply(o, in[j]);
             store(o, dst0 + it * dstep, vec_out);
           }
         }
@@ -515,7 +557,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
         const int row = r0 + it * RPP;
         if (row >= rows) break;
         v4i o = lds_chunk(row);
-        if constexpr (EPI == EPI_GATE) {
+        if constexpr (GATE) {
           o = vec_in ? gate_apply(o, gate_in(row, tok, std::true_type{}))
                      : gate_apply(o, gate_in(row, tok, std::false_type{}));
           next_tok();

@@ -5,7 +5,23 @@
 
 namespace vfa {
 
-enum { EPI_BIAS = 0, EPI_GATE = 2, EPI_LORA = 3, EPI_SWIGLU = 4 };
+// Epilogues.  The LoRA merge (phase 1) combines with the plain store, the
+// gate-residual (phase 2) and the SwiGLU activation (phase 2).
+enum {
+  EPI_BIAS = 0,
+  EPI_GATE = 2,
+  EPI_LORA = 3,
+  EPI_SWIGLU = 4,
+  EPI_LORA_GATE = 5,
+  EPI_SWIGLU_LORA = 6
+};
+constexpr bool epi_lora(int e) { return e == EPI_LORA || e == EPI_LORA_GATE || e == EPI_SWIGLU_LORA; }
+constexpr bool epi_gate(int e) { return e == EPI_GATE || e == EPI_LORA_GATE; }
+constexpr bool epi_swiglu(int e) { return e == EPI_SWIGLU || e == EPI_SWIGLU_LORA; }
+
+// Adapter branches of one LoRA epilogue (the three Q/K/V adapters of a merged
+// projection): output column n belongs to branch n / lora_branch_cols.
+constexpr int LORA_MAX_BRANCHES = 3;
 
 struct GemmParams {
   const uint8_t* a;  // activation codes [m, k], row stride lda bytes
@@ -30,12 +46,17 @@ struct GemmParams {
   int64_t gate_rows;
   const uint16_t* residual;  // EPI_GATE: residual[m * ldr + n]
   int64_t ldr;
-  const uint16_t* lora_t;  // EPI_LORA: t[m * ldt + r], bf16
+  // LoRA epilogues: delta[m, n] = sum_{r < rank} t[m * ldt + b * lora_t_branch + r] *
+  // B[n * ldb + r] for the branch b of column n (0 when lora_branch_cols is 0),
+  // then bf16(delta * lora_scale[b]) and bf16(delta * lora_strength).
+  const uint16_t* lora_t;  // bf16
   int64_t ldt;
-  const uint16_t* lora_b;  // EPI_LORA: B[n * ldb + r], bf16
+  const uint16_t* lora_b;  // bf16, row n of the (stacked) up-projection
   int64_t ldb;
-  int rank;
-  float lora_scale, lora_strength;
+  int rank;  // 1..128
+  int64_t lora_branch_cols;  // 0: one branch; else a multiple of 32
+  int64_t lora_t_branch;     // t columns between branches
+  float lora_scale[LORA_MAX_BRANCHES], lora_strength;
   int64_t half_n;  // EPI_SWIGLU: columns [0, half_n) are values, [half_n, n) gates
   int group_m;  // tile-order group height
 };

@@ -8,7 +8,8 @@
 // (src/vflash/native/h3_fp8_activation.py:12-55) for the base linear, so the
 // adapter's rows need no separate quantization launch.
 //
-// The adapter rank is small (16..128) and K is the model width, so each output
+// The adapter rank is small (at most a few hundred, three stacked Q/K/V
+// adapters of rank 128 at most) and K is the model width, so each output
 // is a dot product of length K and the work per row is tiny: the kernel is
 // latency-bound, and its parallelism has to come from splitting rows, ranks
 // and K.  One 512-thread workgroup owns a 16-row x 16-rank block of t; its 8
@@ -17,7 +18,9 @@
 // v_mfma_f32_16x16x32_bf16 (adapter rows as operand A, activation rows as
 // operand B) from k = 0 upwards, and wave 0 adds the 8 partial blocks in chunk
 // order, t = bf16(((p0 + p1) + p2) + ... + p7).  The chunks depend on K only,
-// so t does not depend on M, on the row block or on the launch.
+// so t does not depend on M, on the row block or on the launch.  A rank that is
+// not a multiple of 16 reads the adapter rows past it as zeros: t columns
+// [rank, ceil16(rank)) are written as zeros (t's row stride covers them).
 //
 // Fused form: every workgroup of a row block loads all of K for its 16 rows,
 // so each takes the rows' maximum |x| (bit-pattern maximum, NaN propagated, as
@@ -41,7 +44,7 @@ constexpr int LD_PREFETCH = 8;  // K steps whose loads are in flight together
 template <bool QUANT>
 __global__ void __launch_bounds__(64 * LD_WAVES) lora_down_blocks(
     const uint16_t* __restrict__ x, int64_t m, int64_t k, int64_t ldx,
-    const uint16_t* __restrict__ a, int rank, uint16_t* __restrict__ t,
+    const uint16_t* __restrict__ a, int rank, uint16_t* __restrict__ t, int64_t ldt,
     uint8_t* __restrict__ codes, float* __restrict__ scales, int64_t m_pad) {
   __shared__ float part[LD_WAVES][4][64];
   __shared__ uint32_t row_max[LD_WAVES][LD_ROWS];
@@ -57,7 +60,8 @@ __global__ void __launch_bounds__(64 * LD_WAVES) lora_down_blocks(
   // Lane (fr, fq) of K step s supplies elements 32 s + 8 fq .. +7 of x row
   // m0 + fr and of adapter row 16 rb + fr (the same K positions for both).
   const v4i* xr = reinterpret_cast<const v4i*>(x + (rok ? row : 0) * ldx);
-  const v4i* ar = reinterpret_cast<const v4i*>(a + (int64_t)(rb * LD_RANKS + fr) * k);
+  const bool aok = rb * LD_RANKS + fr < rank;  // adapter rows past the rank read as zero
+  const v4i* ar = reinterpret_cast<const v4i*>(a + (int64_t)(aok ? rb * LD_RANKS + fr : 0) * k);
   const int64_t steps = (k + 31) / 32;
   const int64_t s0 = steps * wave / LD_WAVES, s1 = steps * (wave + 1) / LD_WAVES;
 
@@ -70,7 +74,7 @@ __global__ void __launch_bounds__(64 * LD_WAVES) lora_down_blocks(
       const int64_t s = c0 + i;
       const bool ok = s < s1 && s * 32 + fq * 8 < k;
       xv[i] = (ok && rok) ? xr[s * 4 + fq] : v4i{};
-      av[i] = ok ? ar[s * 4 + fq] : v4i{};
+      av[i] = (ok && aok) ? ar[s * 4 + fq] : v4i{};
     }
 #pragma unroll
     for (int i = 0; i < LD_PREFETCH; ++i) {
@@ -106,7 +110,7 @@ __global__ void __launch_bounds__(64 * LD_WAVES) lora_down_blocks(
       for (int w = 1; w < LD_WAVES; ++w) v += part[w][i][lane];
       o[i] = f32_to_bf16(v);
     }
-    *reinterpret_cast<uint2*>(t + row * rank + rb * LD_RANKS + 4 * fq) =
+    *reinterpret_cast<uint2*>(t + row * ldt + rb * LD_RANKS + 4 * fq) =
         make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
   }
   if constexpr (!QUANT) return;
@@ -152,22 +156,26 @@ __global__ void __launch_bounds__(64 * LD_WAVES) lora_down_blocks(
   }
 }
 
+// t is [m, ldt] with ldt >= ceil16(rank): every rank block writes its 16 columns.
 hipError_t launch_lora_down(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
-                            const uint16_t* a, int rank, uint16_t* t, hipStream_t s) {
-  if (rank % LD_RANKS) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)((m + LD_ROWS - 1) / LD_ROWS), (unsigned)(rank / LD_RANKS));
-  lora_down_blocks<false><<<grid, 64 * LD_WAVES, 0, s>>>(x, m, k, ldx, a, rank, t, nullptr,
+                            const uint16_t* a, int rank, uint16_t* t, int64_t ldt,
+                            hipStream_t s) {
+  const int blocks = (rank + LD_RANKS - 1) / LD_RANKS;
+  if (rank < 1 || ldt < (int64_t)blocks * LD_RANKS) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((m + LD_ROWS - 1) / LD_ROWS), (unsigned)blocks);
+  lora_down_blocks<false><<<grid, 64 * LD_WAVES, 0, s>>>(x, m, k, ldx, a, rank, t, ldt, nullptr,
                                                          nullptr, m);
   return hipGetLastError();
 }
 
 hipError_t launch_quant_lora(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
-                             const uint16_t* a, int rank, uint16_t* t, uint8_t* codes,
-                             float* scales, int64_t m_pad, hipStream_t s) {
-  if (rank % LD_RANKS || m_pad < m) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)((m_pad + LD_ROWS - 1) / LD_ROWS), (unsigned)(rank / LD_RANKS));
-  lora_down_blocks<true><<<grid, 64 * LD_WAVES, 0, s>>>(x, m, k, ldx, a, rank, t, codes, scales,
-                                                        m_pad);
+                             const uint16_t* a, int rank, uint16_t* t, int64_t ldt,
+                             uint8_t* codes, float* scales, int64_t m_pad, hipStream_t s) {
+  const int blocks = (rank + LD_RANKS - 1) / LD_RANKS;
+  if (rank < 1 || ldt < (int64_t)blocks * LD_RANKS || m_pad < m) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((m_pad + LD_ROWS - 1) / LD_ROWS), (unsigned)blocks);
+  lora_down_blocks<true><<<grid, 64 * LD_WAVES, 0, s>>>(x, m, k, ldx, a, rank, t, ldt, codes,
+                                                        scales, m_pad);
   return hipGetLastError();
 }
 

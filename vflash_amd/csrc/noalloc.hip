@@ -87,7 +87,7 @@ int vflash_fp8_linear_swiglu_quantize_noalloc(const void* a, const float* sa, in
   p.ldo = ldh;
   p.half_n = n / 2;
   p.amax_part = part_max;
-  p.lora_scale = 1.0f;
+  p.lora_scale[0] = p.lora_scale[1] = p.lora_scale[2] = 1.0f;
   p.lora_strength = 1.0f;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (vfa::launch_fp8_gemm(p, vfa::EPI_SWIGLU, s) != hipSuccess) return VFLASH_ELAUNCH;

@@ -7,6 +7,8 @@ No wrapper synchronizes.  Unsupported devices raise ``ValueError``.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from vflash_amd import _lib
@@ -170,10 +172,11 @@ def swiglu_parts(n: int) -> int:
     return int(_lib.library().vflash_swiglu_parts(n))
 
 
-def fp8_gemm_swiglu(codes, act_scale, weight, w_scale, rows, bias=None):
+def fp8_gemm_swiglu(codes, act_scale, weight, w_scale, rows, bias=None, lora=None):
     """h = bf16(value * bf16(silu(gate))) of the packed projection ``weight``
     ([2F, K]: value rows, then gate rows), plus per-row |h| maxima per
-    128-column group."""
+    128-column group.  ``lora`` (``LoraOperands``, B of shape [2F, rank]) merges
+    the adapter delta into value and gate columns before the activation."""
     device = _gemm_operands(codes, act_scale, weight, w_scale, rows, bias)
     n, k = weight.shape
     if n % 256:
@@ -181,9 +184,16 @@ def fp8_gemm_swiglu(codes, act_scale, weight, w_scale, rows, bias=None):
     h = torch.empty((rows, n // 2), device=device, dtype=torch.bfloat16)
     amax = torch.empty((rows, swiglu_parts(n)), device=device, dtype=torch.float32)
     if rows:
-        call("vflash_fp8_linear_swiglu", ptr(codes), ptr(act_scale), codes.stride(0), ptr(weight),
-             ptr(w_scale), weight.stride(0), rows, n, k, ptr(bias), ptr(h), h.stride(0),
-             ptr(amax), stream_of(device))
+        if lora is None:
+            call("vflash_fp8_linear_swiglu", ptr(codes), ptr(act_scale), codes.stride(0), ptr(weight),
+                 ptr(w_scale), weight.stride(0), rows, n, k, ptr(bias), ptr(h), h.stride(0),
+                 ptr(amax), stream_of(device))
+        else:
+            t, ldt, b, ldb = lora.operands(rows, n, device)
+            call("vflash_fp8_linear_swiglu_lora", ptr(codes), ptr(act_scale), codes.stride(0),
+                 ptr(weight), ptr(w_scale), weight.stride(0), rows, n, k, ptr(bias), ptr(t), ldt,
+                 ptr(b), ldb, lora.rank, float(lora.scale), float(lora.strength), ptr(h),
+                 h.stride(0), ptr(amax), stream_of(device))
     return h, amax
 
 
@@ -233,8 +243,9 @@ def requant_rows(g, amax_part, pad_to: int = 16):
 
 
 def fp8_gemm_gate_residual(codes, act_scale, weight, w_scale, rows, gate, residual, bias=None,
-                           out=None, gate_index=None):
-    """out = bf16(residual + bf16(gate * linear)).
+                           out=None, gate_index=None, lora=None):
+    """out = bf16(residual + bf16(gate * linear)), with ``lora`` (``LoraOperands``)
+    linear -> bf16(linear + delta) first (the adapted gate-residual).
 
     ``gate`` is ``[N]`` (one row for every token), ``[T, N]`` with ``rows`` a
     multiple of T (row m uses gate row m % T: ``[rows, N]`` per row, ``[S, N]``
@@ -271,56 +282,125 @@ def fp8_gemm_gate_residual(codes, act_scale, weight, w_scale, rows, gate, residu
           or out.device != device):
         raise ValueError("out must be a BF16 [rows, N] matrix with unit column stride")
     if rows:
-        call("vflash_fp8_linear_gate_residual", ptr(codes), ptr(act_scale), codes.stride(0),
+        t = ldt = b = ldb = None
+        rank, scale, strength = 0, 1.0, 1.0
+        if lora is not None:
+            t, ldt, b, ldb = lora.operands(rows, n, device)
+            rank, scale, strength = lora.rank, float(lora.scale), float(lora.strength)
+        call("vflash_fp8_linear_lora_gate_residual", ptr(codes), ptr(act_scale), codes.stride(0),
              ptr(weight), ptr(w_scale), weight.stride(0), rows, n, k, ptr(bias), ptr(gate), gts,
-             ghs, tokens, ptr(gate_index), gate_rows, ptr(residual), residual.stride(0), ptr(out),
-             out.stride(0), stream_of(device))
+             ghs, tokens, ptr(gate_index), gate_rows, ptr(residual), residual.stride(0), ptr(t),
+             ldt or 0, ptr(b), ldb or 0, rank, scale, strength, ptr(out), out.stride(0),
+             stream_of(device))
     return out
 
 
-def lora_down(x, lora_a):
-    """t = bf16(x . lora_a^T) for a BF16 activation matrix and a BF16 [rank, K] adapter."""
+LORA_MAX_RANK = 128  # per adapter (branch) in the GEMM epilogues
+LORA_DOWN_MAX_RANK = 512  # stacked adapters in one down-projection
+
+
+def _round_up(v: int, q: int) -> int:
+    return -(-v // q) * q
+
+
+def _lora_a(x, lora_a):
     if x.dtype != torch.bfloat16 or x.ndim != 2 or x.stride(1) != 1:
         raise ValueError("LoRA input must be a 2-D BF16 matrix with unit column stride")
-    if lora_a.dtype != torch.bfloat16 or lora_a.ndim != 2 or not lora_a.is_contiguous():
-        raise ValueError("LoRA A must be a contiguous BF16 [rank, K] matrix")
+    if lora_a.dtype != torch.bfloat16 or lora_a.ndim != 2:
+        raise ValueError("LoRA A must be a BF16 [rank, K] matrix")
+    if lora_a.shape[1] != x.shape[1]:
+        raise ValueError("LoRA A does not match the input width")
+    if not 1 <= lora_a.shape[0] <= LORA_DOWN_MAX_RANK:
+        raise ValueError(f"LoRA rank must be 1..{LORA_DOWN_MAX_RANK}")
+    if not lora_a.is_contiguous() or lora_a.data_ptr() % 16:
+        lora_a = lora_a.contiguous().clone()  # the kernel reads whole contiguous rows
+    return lora_a
+
+
+def lora_down(x, lora_a):
+    """t = bf16(x . lora_a^T) for a BF16 activation matrix and a BF16 [rank, K]
+    adapter.  Returns a [M, rank] view of a [M, ceil16(rank)] buffer whose extra
+    columns are zero (the GEMM epilogues read whole 8-element groups)."""
+    lora_a = _lora_a(x, lora_a)
     device = require_device(x, lora_a)
     m, k = x.shape
     rank = lora_a.shape[0]
-    if lora_a.shape[1] != k:
-        raise ValueError("LoRA A does not match the input width")
-    t = torch.empty((m, rank), device=device, dtype=torch.bfloat16)
+    ldt = _round_up(rank, 16)
+    t = torch.empty((m, ldt), device=device, dtype=torch.bfloat16)
     if m:
-        call("vflash_lora_down", ptr(x), m, k, x.stride(0), ptr(lora_a), rank, ptr(t),
+        call("vflash_lora_down", ptr(x), m, k, x.stride(0), ptr(lora_a), rank, ptr(t), ldt,
              stream_of(device))
-    return t
+    return t[:, :rank]
 
 
 def quantize_lora_supported(k: int, rank: int) -> bool:
     """Shapes of the fused quantize + LoRA-down kernel (those of ``lora_down``)."""
-    return k % 16 == 0 and k >= 16 and rank % 16 == 0 and 16 <= rank <= 128
+    return k % 16 == 0 and k >= 16 and 1 <= rank <= LORA_DOWN_MAX_RANK
 
 
 def quantize_rows_lora(x, lora_a, pad_to: int = 16):
     """Codes/scales of ``quantize_rows(x)`` and the ``t`` of ``lora_down(x, lora_a)``
     (both bit-identical) from one launch; see ``quantize_lora_supported`` for the shapes."""
-    if x.dtype != torch.bfloat16 or x.ndim != 2 or x.stride(1) != 1:
-        raise ValueError("LoRA input must be a 2-D BF16 matrix with unit column stride")
-    if lora_a.dtype != torch.bfloat16 or lora_a.ndim != 2 or not lora_a.is_contiguous():
-        raise ValueError("LoRA A must be a contiguous BF16 [rank, K] matrix")
+    lora_a = _lora_a(x, lora_a)
     device = require_device(x, lora_a)
     m, k = x.shape
     rank = lora_a.shape[0]
-    if lora_a.shape[1] != k:
-        raise ValueError("LoRA A does not match the input width")
+    ldt = _round_up(rank, 16)
     m_pad = (m + pad_to - 1) // pad_to * pad_to
     codes = torch.empty((m_pad, k), device=device, dtype=E4M3)
     scales = torch.empty((m_pad, 1), device=device, dtype=torch.float32)
-    t = torch.empty((m, rank), device=device, dtype=torch.bfloat16)
+    t = torch.empty((m, ldt), device=device, dtype=torch.bfloat16)
     if m:
         call("vflash_quantize_rows_lora_e4m3", ptr(x), m, k, x.stride(0), ptr(codes), ptr(scales),
-             m_pad, ptr(lora_a), rank, ptr(t), stream_of(device))
-    return codes, scales, t
+             m_pad, ptr(lora_a), rank, ptr(t), ldt, stream_of(device))
+    return codes, scales, t[:, :rank]
+
+
+def _rows_for_lora(matrix, rows, cols):
+    """``matrix`` ([rows, >= cols] BF16) as the epilogues read it: unit column
+    stride, a row stride that is a multiple of 8 and 16-byte alignment; a copy
+    (zero-padded to a multiple of 8 columns) when it is not.  Returns
+    (tensor, row stride)."""
+    if matrix.dtype != torch.bfloat16 or matrix.ndim != 2 or matrix.shape[0] != rows:
+        raise ValueError("LoRA operands must be BF16 matrices of the declared rows")
+    if matrix.shape[1] < cols:
+        raise ValueError("LoRA operands do not cover the rank")
+    if matrix.stride(1) == 1 and matrix.stride(0) % 8 == 0 and matrix.data_ptr() % 16 == 0:
+        # The epilogue reads each row up to cols rounded up to 8: those elements
+        # must lie inside the tensor's storage (a view [:, :rank] of lora_down's
+        # padded buffer does; a tensor ending at column `cols` of its last row may not).
+        end = matrix.storage_offset() + (rows - 1) * matrix.stride(0) + _round_up(cols, 8)
+        if rows == 0 or end * 2 <= matrix.untyped_storage().nbytes():
+            return matrix, matrix.stride(0)
+    padded = torch.zeros((rows, _round_up(cols, 8)), device=matrix.device, dtype=torch.bfloat16)
+    padded[:, :cols] = matrix[:, :cols]
+    return padded, padded.shape[1]
+
+
+class LoraOperands:
+    """One adapter's operands for a GEMM epilogue: t = bf16(x A^T) ``[rows, rank]``
+    (as ``lora_down`` returns it), B ``[N, rank]``, the scale and the strength
+    (h3_reference_lora.py:80-90: delta = bf16(t B^T), then bf16(delta * scale) if
+    scale != 1 and bf16(delta * strength) if strength != 1)."""
+
+    __slots__ = ("t", "b", "rank", "scale", "strength")
+
+    def __init__(self, t, b, scale=1.0, strength=1.0):
+        if t.ndim != 2 or b.ndim != 2 or t.shape[1] != b.shape[1]:
+            raise ValueError("LoRA operands do not match the projection")
+        self.t, self.b, self.rank = t, b, int(b.shape[1])
+        if not 1 <= self.rank <= LORA_MAX_RANK:
+            raise ValueError(f"LoRA rank must be 1..{LORA_MAX_RANK} per adapter")
+        self.scale, self.strength = float(scale), float(strength)
+
+    def operands(self, rows, n, device):
+        if self.b.shape[0] != n or self.t.shape[0] != rows:
+            raise ValueError("LoRA operands do not match the projection")
+        if self.t.device != device or self.b.device != device:
+            raise ValueError("all operands must share one device")
+        t, ldt = _rows_for_lora(self.t, rows, self.rank)
+        b, ldb = _rows_for_lora(self.b, n, self.rank)
+        return t, ldt, b, ldb
 
 
 def fp8_gemm_lora(codes, act_scale, weight, w_scale, rows, t, lora_b, *, scale=1.0,
@@ -333,17 +413,70 @@ def fp8_gemm_lora(codes, act_scale, weight, w_scale, rows, t, lora_b, *, scale=1
     rank = lora_b.shape[1]
     if t.shape != (rows, rank) or lora_b.shape != (n, rank):
         raise ValueError("LoRA operands do not match the projection")
-    if t.stride(1) != 1 or lora_b.stride(1) != 1:
-        raise ValueError("LoRA operands need unit column stride")
-    if t.device != device or lora_b.device != device:
-        raise ValueError("all operands must share one device")
+    lora = LoraOperands(t, lora_b, scale, strength)
     out = torch.empty((rows, n), device=device, dtype=torch.bfloat16)
     if rows:
+        tt, ldt, bb, ldb = lora.operands(rows, n, device)
         call("vflash_fp8_linear_lora", ptr(codes), ptr(act_scale), codes.stride(0), ptr(weight),
-             ptr(w_scale), weight.stride(0), rows, n, k, ptr(bias), ptr(t), t.stride(0),
-             ptr(lora_b), lora_b.stride(0), rank, float(scale), float(strength), ptr(out),
-             out.stride(0), stream_of(device))
+             ptr(w_scale), weight.stride(0), rows, n, k, ptr(bias), ptr(tt), ldt, ptr(bb), ldb,
+             rank, float(scale), float(strength), ptr(out), out.stride(0), stream_of(device))
     return out
+
+
+def fp8_gemm_lora_branches(codes, act_scale, weight, w_scale, rows, t, t_branch, lora_b, rank,
+                           scales, *, strength=1.0, bias=None, planes=0):
+    """The LoRA linear with ``len(scales)`` (1..3) adapter branches over equal runs
+    of output columns: column c of branch b = c // (N / branches) takes
+    delta = bf16(t[:, b * t_branch : b * t_branch + rank] . lora_b[c]^T), then
+    bf16(delta * scales[b]) and the strength step.  ``t`` is [rows, >= (branches-1)
+    * t_branch + rank] with a row stride that is a multiple of 8; ``lora_b`` is
+    [N, >= rank].  ``planes`` > 0 writes [planes, rows, N / planes] (as
+    ``fp8_gemm_planes``), else [rows, N]."""
+    device = _gemm_operands(codes, act_scale, weight, w_scale, rows, bias)
+    n, k = weight.shape
+    branches = len(scales)
+    if not 1 <= branches <= 3 or n % branches or (branches > 1 and (n // branches) % 32):
+        raise ValueError("adapter branches must split the output into runs of 32-column multiples")
+    if not 1 <= rank <= LORA_MAX_RANK:
+        raise ValueError(f"LoRA rank must be 1..{LORA_MAX_RANK} per adapter")
+    if branches > 1 and (t_branch < rank or t_branch % 8):
+        raise ValueError("t branches must be at least the rank wide, a multiple of 8")
+    if t.device != device or lora_b.device != device:
+        raise ValueError("all operands must share one device")
+    tt, ldt = _rows_for_lora(t, rows, (branches - 1) * t_branch + rank if branches > 1 else rank)
+    if tt is not t and branches > 1:
+        raise ValueError("stacked adapter rows need a row stride that is a multiple of 8")
+    bb, ldb = _rows_for_lora(lora_b, n, rank)
+    if planes:
+        if n % planes:
+            raise ValueError("the merged width must split evenly into planes")
+        cols = n // planes
+        out = torch.empty((planes, rows, cols), device=device, dtype=torch.bfloat16)
+        ldo, plane_cols, plane_stride = cols, cols, rows * cols
+    else:
+        out = torch.empty((rows, n), device=device, dtype=torch.bfloat16)
+        ldo, plane_cols, plane_stride = n, 0, 0
+    if rows:
+        sc = (ctypes.c_float * branches)(*[float(v) for v in scales])
+        call("vflash_fp8_linear_lora_branches", ptr(codes), ptr(act_scale), codes.stride(0),
+             ptr(weight), ptr(w_scale), weight.stride(0), rows, n, k, ptr(bias), ptr(tt), ldt,
+             t_branch if branches > 1 else 0, ptr(bb), ldb, rank, branches, sc, float(strength),
+             ptr(out), ldo, plane_cols, plane_stride, stream_of(device))
+    return out
+
+
+def gemm_tiling(m: int, n: int, compute_units: int = 256, branch_cols: int = 0) -> str:
+    """Name of the tiling the E4M3 GEMM entries use for an m x n output
+    (``vflash_fp8_gemm_tiling``; a host-side query)."""
+    index = _lib.library().vflash_fp8_gemm_tiling(m, n, compute_units, branch_cols)
+    if index < 0:
+        raise ValueError("no tiling for these arguments")
+    return GEMM_TILINGS[index]
+
+
+# The tilings in the order of vflash_fp8_gemm_tiling's result.
+GEMM_TILINGS = ("256x256", "256x192", "256x128", "128x192", "128x128", "128x128 one round",
+                "128x64", "64x64")
 
 
 def nvfp4_gemm(codes, act_scale, packed, block_scales, alpha, rows, bias=None):
