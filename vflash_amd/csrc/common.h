@@ -179,7 +179,6 @@ __device__ __forceinline__ float wave_max(float v) {
 // unsigned maximum of patterns is the maximum of |x|, or NaN when any x is NaN.
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-// acc (two 16-bit |bf16| patterns) updated with the two bf16 of word w.
 // Maximum of v over each 16-lane row of the wave, in every lane of the row:
 // DPP quad permutations [1,0,3,2] and [2,3,0,1], then the half-row and row
 // mirrors (lane i with 7 - i, then with 15 - i).  All lanes must be active.
@@ -191,6 +190,7 @@ __device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
   return v;
 }
 
+// acc (two 16-bit |bf16| patterns) updated with the two bf16 of word w.
 __device__ __forceinline__ uint32_t abs_max_pk(uint32_t acc, uint32_t w) {
   const u16x2 a = __builtin_bit_cast(u16x2, acc), b = __builtin_bit_cast(u16x2, w & 0x7fff7fffu);
   return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(a, b));

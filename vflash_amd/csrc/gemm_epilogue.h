@@ -516,8 +516,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
       // before any is stored, so each latency is paid once
       // per batch, not once per row.  The swizzle of row r0 + it * RPP repeats
       // every four passes, so four LDS offsets and one output row step serve
-      // every pass.  Rows past BM (CH = 24: 26 passes of 10 rows) read inside
-      // the ring and are neither loaded from global memory nor stored.
+      // every pass.  With CH = 24 (26 passes of 10 rows) the last pass reaches
+      // rows up to 259: those past BM are read from LDS (at most 100 KB into the
+      // 112 KB ring) but neither loaded from global memory nor stored; the
+      // batch's passes past the last (26..31) read nothing.
       static_assert((4 * RPP) % SWZ == 0, "the swizzle repeats every four passes");
       constexpr int BATCH = PASSES < 8 ? PASSES : 8;
       int lofs[4];
@@ -533,7 +535,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
         for (int j = 0; j < BATCH; ++j) {
           const int it = it0 + j;
           const int row = r0 + it * RPP;
-          v[j] = *reinterpret_cast<const v4i*>(stage + lofs[it & 3] + it * RPP * PITCH);
+          if (it < PASSES)  // a constant: the loop is unrolled
+            v[j] = *reinterpret_cast<const v4i*>(stage + lofs[it & 3] + it * RPP * PITCH);
           if constexpr (GATE) {
             if (it < PASSES && (PASSES * RPP == BM || row < BM))
               in[j] = gate_in(row, tok, std::true_type{});
