@@ -154,15 +154,26 @@ def cpu_oracle_linear(x, codes, scale, b, flops_per_row):
 
 
 def cpu_baseline_weight_only(x, codes, scale, b, flops_per_row):
-    """The reference's CPU weight-only path on a bounded row sample."""
+    """The reference's CPU weight-only path: every row of the workload (the whole
+    call, weight restore included, as the reference makes it), or a row sample
+    when a probe predicts more than about 8 s per call on this host."""
     from oracle.baseline import weight_only_linear
 
     threads = use_host_threads()
-    rows = 128
-    t0 = time.perf_counter()
-    weight_only_linear(x[:rows], codes, scale, b)
-    probe = time.perf_counter() - t0
-    rows = int(min(x.shape[0], max(128, 128 * 4.0 / max(probe, 1e-3))) // 128 * 128)
+
+    def timed(r):
+        t0 = time.perf_counter()
+        weight_only_linear(x[:r], codes, scale, b)
+        return time.perf_counter() - t0
+
+    # Two probes give the per-call cost (the weight restore) and the per-row cost.
+    timed(128)
+    t1, t2 = timed(128), timed(640)
+    per_row = max((t2 - t1) / 512, 1e-9)
+    if t1 + per_row * (x.shape[0] - 128) <= 8.0:
+        rows = x.shape[0]
+    else:
+        rows = int(min(x.shape[0], max(128, 4.0 / per_row)) // 128 * 128)
     sample = x[:rows]
     weight_only_linear(sample, codes, scale, b)  # warm-up
     times = []
