@@ -115,8 +115,8 @@ hipError_t launch_fp8_gemm(const GemmParams& params, int epi, hipStream_t s) {
   if (epi_swiglu(epi)) {
     // One tiling: 128 value + 128 gate columns, the 256x256 schedule.
     p.group_m = tiling_group_m(GEMM_256x256, (p.half_n + 127) / 128);
-    if (epi == EPI_SWIGLU_LORA) return launch_pipe<EPI_SWIGLU_LORA, PipeCfg<256, 256, 2, 0>>(p, s);
-    return launch_pipe<EPI_SWIGLU, PipeCfg<256, 256, 2, 0>>(p, s);
+    if (epi == EPI_SWIGLU_LORA) return launch_pipe<EPI_SWIGLU_LORA, PipeCfg<256, 256, SPLIT_RING, 0>>(p, s);
+    return launch_pipe<EPI_SWIGLU, PipeCfg<256, 256, SPLIT_RING, 0>>(p, s);
   }
   const int tiling =
       pick_tiling(p.m, p.n, compute_units(), epi_lora(epi) ? p.lora_branch_cols : 0);

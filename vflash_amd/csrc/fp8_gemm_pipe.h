@@ -33,11 +33,23 @@ namespace vfa {
 //   and with the reads of stage kt+1 substep 0.
 // NS - 1 stages are in flight while one is multiplied; rows are stored with
 // the lds_swizzle chunk permutation.
-// Ring bytes of an NS-slot ring for a BM x BN tile.
-constexpr int pipe_lds(int bm, int bn, int ns) { return ns * (bm + bn) * 128; }
+//
+// NS = SPLIT_RING selects a split ring instead: two activation slots and three
+// weight slots (160 KB for 256 x 256).  The weight DMAs of stage kt+2 then go
+// into the slot freed at the barrier of stage kt-1, issued during the first
+// half of stage kt, and only the activation DMAs wait for the barrier of stage
+// kt: the stage's DMA instructions are spread over both halves instead of
+// all crowding the second.  The scale and bias vectors (and the SwiGLU silu
+// table) are DMA'd during the last stage into the third weight slot, which the
+// output staging tile does not cover.
+constexpr int SPLIT_RING = 0;
+// Ring bytes of an NS-slot ring (or of the split ring) for a BM x BN tile.
+constexpr int pipe_lds(int bm, int bn, int ns) {
+  return ns == SPLIT_RING ? (2 * bm + 3 * bn) * 128 : ns * (bm + bn) * 128;
+}
 // Workgroups per CU the LDS allows (at most two).
 constexpr int pipe_occupancy(int bm, int bn, int ns) {
-  return 2 * (pipe_lds(bm, bn, ns) + VEC_LDS) <= 160 * 1024 ? 2 : 1;
+  return 2 * (pipe_lds(bm, bn, ns) + (ns == SPLIT_RING ? 0 : VEC_LDS)) <= 160 * 1024 ? 2 : 1;
 }
 
 // SDMA: K % 128 == 0; in full tiles the DMA advances K through the scalar
@@ -49,14 +61,19 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
                                           int wave) {
   constexpr int BK = 128, WGM = 2, WGN = 2;
   constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
+  constexpr bool SPLIT = NS == SPLIT_RING;
   constexpr int HA = BM * BK;              // activation rows of one stage
+  constexpr int HW = BN * BK;              // weight rows of one stage
   constexpr int SLOT = (BM + BN) * BK;     // one stage: activation rows, then weight rows
   constexpr int DMA_A = BM / 32;           // one-KB DMA instructions per wave, activation rows
   constexpr int DMA_W = BN / 32;           // and weight rows
   constexpr int DMA = DMA_A + DMA_W;       // per wave per stage
   static_assert(MB >= 1 && NB >= 1 && WM % 32 == 0 && WN % 32 == 0, "32x32 blocks per wave");
-  static_assert(NS * SLOT == pipe_lds(BM, BN, NS), "slot layout");
-  static_assert(NS >= 2 && (NS - 1) * DMA < 64, "vmcnt range");
+  static_assert(SPLIT ? 2 * HA + 3 * HW == pipe_lds(BM, BN, NS) : NS * SLOT == pipe_lds(BM, BN, NS),
+                "slot layout");
+  static_assert(SPLIT || (NS >= 2 && (NS - 1) * DMA < 64), "vmcnt range");
+  static_assert(!SPLIT || 2 * HA + 2 * HW >= BM * BN * 2, "the output staging tile leaves the "
+                "third weight slot to the vectors");
   static_assert(DMA_A % 2 == 0 && DMA_W % 2 == 0,
                 "blocks alternate between the two swizzle parities");
 
@@ -108,74 +125,88 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
   const uint32_t w_base1 = (uint32_t)((wrow0 + 8) * p.ldw + dch1 * 16);
   const uint32_t a_step = (uint32_t)(16 * p.lda), w_step = (uint32_t)(16 * p.ldw);
   const int KT = (int)((p.k + BK - 1) / BK);
-  const uint32_t a_lds = ring_lds + wave * DMA_A * 1024;       // this wave's activation blocks
-  const uint32_t w_lds = ring_lds + HA + wave * DMA_W * 1024;  // and weight blocks
+  const uint32_t a_lds = ring_lds + wave * DMA_A * 1024;  // this wave's activation blocks
+  const uint32_t w_lds = ring_lds + wave * DMA_W * 1024;  // and weight blocks (+ slot offset)
+  // Ring offsets of activation slot ja and weight slot jw: in the shared ring
+  // slot j holds the activation rows, then the weight rows, of one stage; the
+  // split ring has two activation slots, then three weight slots.
+  auto a_slot = [](int ja) { return (uint32_t)(SPLIT ? ja * HA : ja * SLOT); };
+  auto w_slot = [](int jw) { return (uint32_t)(SPLIT ? 2 * HA + jw * HW : jw * SLOT + HA); };
 
-  // DMA of stage s into slot j: instruction i < DMA_A is A block i, the rest W
-  // blocks; chunks past K (and whole stages past the end) read as zeros.
+  // DMA of stage s into activation slot ja and weight slot jw: instruction
+  // i < DMA_A is A block i, the rest W blocks; chunks past K (and whole stages
+  // past the end) read as zeros.
   struct Dma {
-    uint32_t slot, kb, kill0, kill1;
+    uint32_t aslot, wslot, kb, kill0, kill1;
   };
-  auto dma_setup = [&](int j, int s) {
+  auto dma_setup = [&](int ja, int jw, int s) {
     const uint32_t kb = (uint32_t)s * BK;
-    return Dma{(uint32_t)(j * SLOT), kb, ((int64_t)kb + dch0 * 16 < p.k) ? 0u : VFA_OOB,
+    return Dma{a_slot(ja), w_slot(jw), kb, ((int64_t)kb + dch0 * 16 < p.k) ? 0u : VFA_OOB,
                ((int64_t)kb + dch1 * 16 < p.k) ? 0u : VFA_OOB};
   };
   auto dma_one = [&](const Dma& d, auto i) {
     if constexpr (i < DMA_A) {
       const uint32_t off = (i % 2 ? a_base1 : a_base0) + (i / 2) * a_step + d.kb;
-      lds_dma16(ra, a_lds + d.slot + i * 1024, off | (i % 2 ? d.kill1 : d.kill0));
+      lds_dma16(ra, a_lds + d.aslot + i * 1024, off | (i % 2 ? d.kill1 : d.kill0));
     } else {
       constexpr int w = i - DMA_A;
       const uint32_t off = (w % 2 ? w_base1 : w_base0) + (w / 2) * w_step + d.kb;
-      lds_dma16(rw, w_lds + d.slot + w * 1024, off | (w % 2 ? d.kill1 : d.kill0));
+      lds_dma16(rw, w_lds + d.wslot + w * 1024, off | (w % 2 ? d.kill1 : d.kill0));
     }
   };
   // Scalar-offset form (SDMA): resources are selected per stage.
   const __amdgpu_buffer_rsrc_t ra_none = make_rsrc(p.a, 0u), rw_none = make_rsrc(p.w, 0u);
   struct SDma {
     __amdgpu_buffer_rsrc_t ra, rw;
-    uint32_t slot, kb;
+    uint32_t aslot, wslot, kb;
   };
-  auto sdma_setup = [&](int j, int s) {
+  auto sdma_setup = [&](int ja, int jw, int s) {
     const bool live = s < KT;
-    return SDma{live ? ra : ra_none, live ? rw : rw_none, (uint32_t)(j * SLOT),
+    return SDma{live ? ra : ra_none, live ? rw : rw_none, a_slot(ja), w_slot(jw),
                 live ? (uint32_t)s * BK : 0u};
   };
   auto sdma_one = [&](const SDma& d, auto i) {
     if constexpr (i < DMA_A) {
-      lds_dma16_so(d.ra, a_lds + d.slot + i * 1024, i % 2 ? a_base1 : a_base0,
+      lds_dma16_so(d.ra, a_lds + d.aslot + i * 1024, i % 2 ? a_base1 : a_base0,
                    d.kb + (i / 2) * a_step);
     } else {
       constexpr int w = i - DMA_A;
-      lds_dma16_so(d.rw, w_lds + d.slot + w * 1024, w % 2 ? w_base1 : w_base0,
+      lds_dma16_so(d.rw, w_lds + d.wslot + w * 1024, w % 2 ? w_base1 : w_base0,
                    d.kb + (w / 2) * w_step);
     }
   };
-  auto issue = [&](int j, int s, auto use_sdma) {
+  // DMA instructions i0 .. i1-1 of stage s.
+  auto issue_range = [&](int ja, int jw, int s, auto use_sdma, auto i0, auto i1) {
     if constexpr (use_sdma) {
-      const SDma d = sdma_setup(j, s);
-      static_for<DMA>([&](auto i) { sdma_one(d, i); });
+      const SDma d = sdma_setup(ja, jw, s);
+      static_for<i1 - i0>([&](auto t) { sdma_one(d, std::integral_constant<int, i0 + t>{}); });
     } else {
-      const Dma d = dma_setup(j, s);
-      static_for<DMA>([&](auto i) { dma_one(d, i); });
+      const Dma d = dma_setup(ja, jw, s);
+      static_for<i1 - i0>([&](auto t) { dma_one(d, std::integral_constant<int, i0 + t>{}); });
     }
+  };
+  using IDA = std::integral_constant<int, DMA_A>;
+  using IDMA = std::integral_constant<int, DMA>;
+  auto issue = [&](int ja, int jw, int s, auto use_sdma) {
+    issue_range(ja, jw, s, use_sdma, std::integral_constant<int, 0>{}, IDMA{});
   };
 
   const int fr = lane & 31, fh = lane >> 5;
   const int fsw = lds_swizzle(fr);
   v8i F[2][MB + NB];  // [K-substep][activation blocks, then weight blocks]
-  // Fragments of K-substep ks of the stage in slot j into register set ks.
-  auto read_one = [&](int j, auto ks, auto f) {
+  // Fragments of K-substep ks of the stage in slots ja / jw into register set ks.
+  auto read_one = [&](int ja, int jw, auto ks, auto f) {
     const int cc = ks * 4 + fh * 2;
     const int o0 = (cc ^ fsw) << 4, o1 = ((cc + 1) ^ fsw) << 4;
-    const uint8_t* src = f < MB ? ring + j * SLOT + (wm * WM + fr) * BK + f * 32 * BK
-                                : ring + j * SLOT + HA + (wn * WN + fr) * BK + (f - MB) * 32 * BK;
+    const uint8_t* src = f < MB ? ring + a_slot(ja) + (wm * WM + fr) * BK + f * 32 * BK
+                                : ring + w_slot(jw) + (wn * WN + fr) * BK + (f - MB) * 32 * BK;
     const v4i lo = *reinterpret_cast<const v4i*>(src + o0);
     const v4i hi = *reinterpret_cast<const v4i*>(src + o1);
     F[ks][f] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   };
-  auto read = [&](int j, auto ks) { static_for<MB + NB>([&](auto f) { read_one(j, ks, f); }); };
+  auto read = [&](int ja, int jw, auto ks) {
+    static_for<MB + NB>([&](auto f) { read_one(ja, jw, ks, f); });
+  };
   v16f acc[NB][MB];
   static_for<NB>([&](auto i) { static_for<MB>([&](auto jj) { acc[i][jj] = v16f{}; }); });
   // MFMAs number q0..q1-1 of K-substep ks (q = nb * MB + mb).
@@ -208,11 +239,11 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
   // Prologue and K loop; use_sdma selects the scalar-offset DMA (full tiles).
   auto main_loop = [&](auto use_sdma) {
     stage_vectors<BM, BN, epi_swiglu(EPI)>(p, m0, n0, wave, lane, vec_lds);
-    static_for<NS>([&](auto s) { issue((int)s, (int)s, use_sdma); });
+    static_for<NS>([&](auto s) { issue((int)s, (int)s, (int)s, use_sdma); });
     wait_vmcnt<(NS - 1) * DMA, true>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    read(I0{}, I0{});
+    read(0, 0, I0{});
     // The first fragments have landed before the loop: the compiler's wait
     // tracking then sees the same pending LDS reads on both loop entries and
     // waits only for the fragments each MFMA needs.
@@ -222,7 +253,7 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
       const int jn = j + 1 == NS ? 0 : j + 1;  // slot of stage kt + 1
       // Substep 0 of stage kt, while reading substep 1 of the same stage.
       mfmas(I0{}, I0{}, std::integral_constant<int, Q>{});
-      read(j, I1{});
+      read(j, j, I1{});
       interleave(std::integral_constant<int, (RD < Q ? RD : Q)>{});
       mfmas(I1{}, I0{}, std::integral_constant<int, QB>{});
       // The MFMAs above stay above the wait (they keep the MFMA pipe busy while
@@ -238,8 +269,8 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
       // instructions of stage kt+NS and by the reads of one fragment of stage
       // kt+1 (unused after the last stage), so DMA issue and reads overlap the
       // MFMA pipe.
-      const Dma d = dma_setup(j, kt + NS);
-      const SDma sd = sdma_setup(j, kt + NS);
+      const Dma d = dma_setup(j, j, kt + NS);
+      const SDma sd = sdma_setup(j, j, kt + NS);
       static_for<QA>([&](auto i) {
         constexpr int q = QB + i, nb = q / MB, mb = q % MB;
         acc[nb][mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
@@ -252,23 +283,97 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
           else
             dma_one(d, std::integral_constant<int, di>{});
         });
-        if constexpr (i < MB + NB) read_one(jn, I0{}, i);
+        if constexpr (i < MB + NB) read_one(jn, jn, I0{}, i);
         __builtin_amdgcn_sched_barrier(0);
       });
       // Fragments not covered above (smaller tiles have fewer MFMAs than fragments).
       static_for<(MB + NB > QA ? MB + NB - QA : 0)>([&](auto i) {
-        read_one(jn, I0{}, std::integral_constant<int, QA + i>{});
+        read_one(jn, jn, I0{}, std::integral_constant<int, QA + i>{});
       });
       j = jn;
     }
   };
+
+  // The split ring's prologue and K loop.  Stage s sits in activation slot s % 2
+  // and weight slot (s + c) % 3, with c = (1 - KT) mod 3 so that the last
+  // stage's free weight slot, where the vectors go, is always slot 2.
+  auto split_loop = [&](auto use_sdma) {
+    const int c = ((1 - KT) % 3 + 3) % 3;
+    issue(0, c, 0, use_sdma);
+    issue(1, c == 2 ? 0 : c + 1, 1, use_sdma);
+    wait_vmcnt<DMA, true>();  // stage 0 has landed (stage 1 may be in flight)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    read(0, c, I0{});
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt/expcnt untouched
+    // One stage; `last` replaces the weight DMAs of stage kt+2 (past the end)
+    // with the vectors' DMA into weight slot 2.
+    auto stage = [&](int kt, int ja, int jw, auto last) {
+      const int jan = ja ^ 1, jwn = jw == 2 ? 0 : jw + 1, jwf = jwn == 2 ? 0 : jwn + 1;
+      // First half: the MFMAs of substep 0, each with the reads of one
+      // substep-1 fragment and its share of the weight DMAs of stage kt+2 (into
+      // the slot of stage kt-1, free since the last barrier).
+      static_for<Q>([&](auto i) {
+        constexpr int nb = i / MB, mb = i % MB;
+        acc[nb][mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+            F[0][MB + nb], F[0][mb], acc[nb][mb], 0, 0, 0, 0, 0, 0);
+        if constexpr (i < MB + NB) read_one(ja, jw, I1{}, i);
+        if constexpr (!last) {
+          constexpr int d0 = DMA_A + i * DMA_W / Q, d1 = DMA_A + (i + 1) * DMA_W / Q;
+          issue_range(ja, jwf, kt + 2, use_sdma, std::integral_constant<int, d0>{},
+                      std::integral_constant<int, d1>{});
+        } else if constexpr (i == 0) {
+          stage_vectors<BM, BN, epi_swiglu(EPI)>(p, m0, n0, wave, lane, vec_lds);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      static_for<(MB + NB > Q ? MB + NB - Q : 0)>([&](auto i) {
+        read_one(ja, jw, I1{}, std::integral_constant<int, Q + i>{});
+      });
+      // Stage kt+1 has landed for every wave (the weight DMAs of stage kt+2 may
+      // still be in flight); stage kt is fully read.
+      wait_vmcnt<DMA_W, true>();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      // Second half: the MFMAs of substep 1, each with its share of the
+      // activation DMAs of stage kt+2 (into the slot of stage kt) and the reads
+      // of one fragment of stage kt+1.
+      static_for<Q>([&](auto i) {
+        constexpr int nb = i / MB, mb = i % MB;
+        acc[nb][mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+            F[1][MB + nb], F[1][mb], acc[nb][mb], 0, 0, 0, 0, 0, 0);
+        constexpr int d0 = i * DMA_A / Q, d1 = (i + 1) * DMA_A / Q;
+        issue_range(ja, jwf, kt + 2, use_sdma, std::integral_constant<int, d0>{},
+                    std::integral_constant<int, d1>{});
+        if constexpr (i < MB + NB) read_one(jan, jwn, I0{}, i);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      static_for<(MB + NB > Q ? MB + NB - Q : 0)>([&](auto i) {
+        read_one(jan, jwn, I0{}, std::integral_constant<int, Q + i>{});
+      });
+    };
+    int ja = 0, jw = c;
+    for (int kt = 0; kt < KT - 1; ++kt) {
+      stage(kt, ja, jw, std::false_type{});
+      ja ^= 1;
+      jw = jw == 2 ? 0 : jw + 1;
+    }
+    stage(KT - 1, ja, jw, std::true_type{});
+  };
+  auto run = [&](auto use_sdma) {
+    if constexpr (SPLIT)
+      split_loop(use_sdma);
+    else
+      main_loop(use_sdma);
+  };
   if constexpr (SDMA) {
     if (full)
-      main_loop(std::true_type{});
+      run(std::true_type{});
     else
-      main_loop(std::false_type{});
+      run(std::false_type{});
   } else {
-    main_loop(std::false_type{});
+    run(std::false_type{});
   }
   wait_vmcnt<0, true>();  // every DMA has landed before the ring is reused
   __builtin_amdgcn_s_barrier();
@@ -280,7 +385,16 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
 template <int EPI, int BM, int BN, int NS, int PRE, bool SDMA>
 __global__ void __launch_bounds__(256, pipe_occupancy(BM, BN, NS)) fp8_gemm_pipe(const GemmParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t ring[pipe_lds(BM, BN, NS)];
-  __shared__ __attribute__((aligned(1024))) uint8_t vec[VEC_LDS + (epi_swiglu(EPI) ? SILU_LDS : 0)];
+  constexpr int VEC_BYTES = VEC_LDS + (epi_swiglu(EPI) ? SILU_LDS : 0);
+  uint8_t* vec;
+  if constexpr (NS == SPLIT_RING) {
+    // The split ring keeps the vectors in its third weight slot.
+    static_assert(VEC_BYTES <= BN * 128, "vectors fit one weight slot");
+    vec = ring + (2 * BM + 2 * BN) * 128;
+  } else {
+    __shared__ __attribute__((aligned(1024))) uint8_t vec_own[VEC_BYTES];
+    vec = vec_own;
+  }
   int tm, tn;
   // SwiGLU tiles cover BN/2 value columns and their BN/2 gate columns.
   const int64_t tile_cols =
@@ -304,8 +418,11 @@ static hipError_t launch_pipe(const GemmParams& p, hipStream_t s) {
   const int64_t tile_cols =
       epi_swiglu(EPI) ? (p.half_n + C::BN / 2 - 1) / (C::BN / 2) : (p.n + C::BN - 1) / C::BN;
   const dim3 grid((unsigned)(((p.m + C::BM - 1) / C::BM) * tile_cols));
+  // K not a multiple of 128 takes the vector-offset DMA everywhere; there the
+  // split ring's extra lane offsets spill, so such shapes keep the two-slot ring.
+  constexpr int NS_VOFF = C::NS == SPLIT_RING ? 2 : C::NS;
   if (p.k % 128)
-    fp8_gemm_pipe<EPI, C::BM, C::BN, C::NS, C::PRE, false><<<grid, dim3(256), 0, s>>>(p);
+    fp8_gemm_pipe<EPI, C::BM, C::BN, NS_VOFF, C::PRE, false><<<grid, dim3(256), 0, s>>>(p);
   else
     fp8_gemm_pipe<EPI, C::BM, C::BN, C::NS, C::PRE, true><<<grid, dim3(256), 0, s>>>(p);
   return hipGetLastError();
@@ -327,7 +444,7 @@ enum {
 template <int EPI>
 hipError_t launch_tiling(const GemmParams& p, int tiling, hipStream_t s) {
   switch (tiling) {
-    case GEMM_256x256: return launch_pipe<EPI, PipeCfg<256, 256, 2, 0>>(p, s);
+    case GEMM_256x256: return launch_pipe<EPI, PipeCfg<256, 256, SPLIT_RING, 0>>(p, s);
     case GEMM_256x192: return launch_pipe<EPI, PipeCfg<256, 192, 2, 0>>(p, s);
     case GEMM_256x128: return launch_pipe<EPI, PipeCfg<256, 128, 3, 0>>(p, s);
     case GEMM_128x192: return launch_pipe<EPI, PipeCfg<128, 192, 3, 0>>(p, s);
