@@ -205,7 +205,10 @@ __device__ __forceinline__ void stage_vectors(const GemmParams& p, int64_t m0, i
 // stage_vectors (true), or from global memory (false).
 // lora_d: for the LoRA epilogues, the per-block LoRA products computed ahead of
 // the main loop ([nb * MB + mb], same layout as acc), or null to compute them here.
-template <int BM, int BN, int WGM, int WGN, int EPI, bool VEC = false>
+// SW_SCALAR: one weight scale for every column (sw[0], the E2M1-weight GEMM's
+// alpha) instead of one per column; a compile-time choice, so the per-value
+// scale needs no select.
+template <int BM, int BN, int WGM, int WGN, int EPI, bool VEC = false, bool SW_SCALAR = false>
 __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
                                               v16f (&acc)[BN / WGN / 32][BM / WGM / 32],
                                               int64_t m0, int64_t n0, int wm, int wn, int tid,
@@ -239,8 +242,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
       sam[mb] = m0 + row < p.m ? sa_p[m0 + row] : 0.0f;
     }
   });
-  const bool sw_vector = p.sw_step != 0;
-  const float sw0 = VEC ? reinterpret_cast<const float*>(vec)[0] : 0.0f;
+  const float sw0 = VEC && SW_SCALAR ? reinterpret_cast<const float*>(vec)[0] : 0.0f;
 
   // Phase 1, column-block major: the scale and bias of one 32-column block (4
   // columns per g for this lane) are live while its MB row blocks are written.
@@ -270,7 +272,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
           const v4f s4 = s4r[nb][g];
           const uint2 b4 = b4r[nb][g];
           static_for<4>([&](auto i) {
-            sv[g][i] = sw_vector ? s4[(int)i] : sw0;
+            sv[g][i] = SW_SCALAR ? sw0 : s4[(int)i];
             const uint32_t bw = i < 2 ? b4.x : b4.y;
             bv[g][i] = i % 2 ? bf16_hi(bw) : bf16_lo(bw);
           });

@@ -272,7 +272,8 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
   wait_vmcnt<0, true>();  // every DMA has landed before the ring becomes the staging tile
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  gemm_epilogue<256, 256, 2, 2, EPI_BIAS, true>(p, acc, m0, n0, wm, wn, (int)threadIdx.x, ring, vec);
+  gemm_epilogue<256, 256, 2, 2, EPI_BIAS, true, true>(p, acc, m0, n0, wm, wn, (int)threadIdx.x, ring,
+                                                    vec);
 }
 
 hipError_t launch_nvfp4_w4a4(const uint8_t* a, int64_t lda, const uint8_t* as, const uint8_t* w,
