@@ -103,6 +103,16 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
   return __uint_as_float(__float_as_uint(v) | s);
 }
 
+// The lane's index in its wave, computed afresh: the volatile statement is not
+// merged with an earlier computation, so a value needed before and after a long
+// loop is recomputed instead of holding a register through the loop.
+__device__ __forceinline__ int lane_id_fresh() {
+  int lo, lane;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0" : "=v"(lo));
+  asm volatile("v_mbcnt_hi_u32_b32 %0, -1, %1" : "=v"(lane) : "v"(lo));
+  return lane;
+}
+
 // Raw buffer resources: loads outside [0, num_records) return zero and stores
 // there are dropped, which gives free bounds checks at tile edges.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {

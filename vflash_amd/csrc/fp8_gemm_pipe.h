@@ -307,8 +307,10 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
     read(0, c, I0{});
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt/expcnt untouched
     // One stage; `last` replaces the weight DMAs of stage kt+2 (past the end)
-    // with the vectors' DMA into weight slot 2.
-    auto stage = [&](int kt, int ja, int jw, auto last) {
+    // with the vectors' DMA into weight slot 2; `first` starts the accumulators
+    // from the MFMAs of its substep 0 (a zero accumulator operand), so no
+    // instruction zeroes them beforehand.
+    auto stage = [&](int kt, int ja, int jw, auto last, auto first) {
       const int jan = ja ^ 1, jwn = jw == 2 ? 0 : jw + 1, jwf = jwn == 2 ? 0 : jwn + 1;
       // First half: the MFMAs of substep 0, each with the reads of one
       // substep-1 fragment and its share of the weight DMAs of stage kt+2 (into
@@ -316,14 +318,14 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
       static_for<Q>([&](auto i) {
         constexpr int nb = i / MB, mb = i % MB;
         acc[nb][mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-            F[0][MB + nb], F[0][mb], acc[nb][mb], 0, 0, 0, 0, 0, 0);
+            F[0][MB + nb], F[0][mb], first ? v16f{} : acc[nb][mb], 0, 0, 0, 0, 0, 0);
         if constexpr (i < MB + NB) read_one(ja, jw, I1{}, i);
         if constexpr (!last) {
           constexpr int d0 = DMA_A + i * DMA_W / Q, d1 = DMA_A + (i + 1) * DMA_W / Q;
           issue_range(ja, jwf, kt + 2, use_sdma, std::integral_constant<int, d0>{},
                       std::integral_constant<int, d1>{});
         } else if constexpr (i == 0) {
-          stage_vectors<BM, BN, epi_swiglu(EPI)>(p, m0, n0, wave, lane, vec_lds);
+          stage_vectors<BM, BN, epi_swiglu(EPI)>(p, m0, n0, wave, lane_id_fresh(), vec_lds);
         }
         __builtin_amdgcn_sched_barrier(0);
       });
@@ -353,13 +355,18 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
         read_one(jan, jwn, I0{}, std::integral_constant<int, Q + i>{});
       });
     };
-    int ja = 0, jw = c;
-    for (int kt = 0; kt < KT - 1; ++kt) {
-      stage(kt, ja, jw, std::false_type{});
+    if (KT == 1) {
+      stage(0, 0, c, std::true_type{}, std::true_type{});
+      return;
+    }
+    stage(0, 0, c, std::false_type{}, std::true_type{});
+    int ja = 1, jw = c == 2 ? 0 : c + 1;
+    for (int kt = 1; kt < KT - 1; ++kt) {
+      stage(kt, ja, jw, std::false_type{}, std::false_type{});
       ja ^= 1;
       jw = jw == 2 ? 0 : jw + 1;
     }
-    stage(KT - 1, ja, jw, std::true_type{});
+    stage(KT - 1, ja, jw, std::true_type{}, std::false_type{});
   };
   auto run = [&](auto use_sdma) {
     if constexpr (SPLIT)
@@ -378,8 +385,10 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
   wait_vmcnt<0, true>();  // every DMA has landed before the ring is reused
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  gemm_epilogue<BM, BN, WGM, WGN, EPI, true>(p, acc, m0, n0, wm, wn, tid_v, ring, vec,
-                                             LORA_PRE ? lora_d : nullptr);
+  // The thread index after the loop, recomputed rather than held through it.
+  gemm_epilogue<BM, BN, WGM, WGN, EPI, true>(p, acc, m0, n0, wm, wn,
+                                             SPLIT ? wave * 64 + lane_id_fresh() : tid_v, ring,
+                                             vec, LORA_PRE ? lora_d : nullptr);
 }
 
 template <int EPI, int BM, int BN, int NS, int PRE, bool SDMA>
