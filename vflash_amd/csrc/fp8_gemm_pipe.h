@@ -35,7 +35,7 @@ namespace vfa {
 // the lds_swizzle chunk permutation.
 //
 // NS = SPLIT_RING selects a split ring instead: two activation slots and three
-// weight slots (160 KB for 256 x 256).  The weight DMAs of stage kt+2 then go
+// weight slots (160 KB for 256 x 256, 136 KB for 256 x 192).  The weight DMAs of stage kt+2 then go
 // into the slot freed at the barrier of stage kt-1, issued during the first
 // half of stage kt, and only the activation DMAs wait for the barrier of stage
 // kt: the stage's DMA instructions are spread over both halves instead of
@@ -454,7 +454,7 @@ template <int EPI>
 hipError_t launch_tiling(const GemmParams& p, int tiling, hipStream_t s) {
   switch (tiling) {
     case GEMM_256x256: return launch_pipe<EPI, PipeCfg<256, 256, SPLIT_RING, 0>>(p, s);
-    case GEMM_256x192: return launch_pipe<EPI, PipeCfg<256, 192, 2, 0>>(p, s);
+    case GEMM_256x192: return launch_pipe<EPI, PipeCfg<256, 192, SPLIT_RING, 0>>(p, s);
     case GEMM_256x128: return launch_pipe<EPI, PipeCfg<256, 128, 3, 0>>(p, s);
     case GEMM_128x192: return launch_pipe<EPI, PipeCfg<128, 192, 3, 0>>(p, s);
     case GEMM_128x128: return launch_pipe<EPI, PipeCfg<128, 128, 2, -1>>(p, s);
