@@ -140,37 +140,49 @@ def silu_bf16(bits: int) -> int:
     return _bf16_bits_of_double(_f32_of_fraction(Fraction(g) / Fraction(d)))
 
 
-# The silu window: bf16 magnitudes 2^-9 <= |g| < 2^7 (bit patterns 0x3B00 ..
-# 0x42FF without the sign), 2048 per sign.  Outside it the function is
-# bf16(g / 2) below, g above for g > 0 and g * 0 above for g < 0; the kernel
-# computes those and looks the window up (tests/test_silu_table.py checks the
-# whole rule against the oracle on every bf16 value).
+# The silu window: bf16 magnitudes 2^-9 <= |g| <= 126.5 (bit patterns 0x3B00 ..
+# 0x42FD without the sign), SILU_N per sign.  Outside it the function is
+# bf16(g / 2) below, g above for g > 0 and g * 0 above for g < 0.  Each sign's
+# table holds a below-window entry, the window, and an above-window entry
+# (SILU_STRIDE entries); an entry is the bf16 pattern of silu(g) in its high
+# half (T) and a bf16 factor M in its low half, so that every bf16 g gives
+# bf16(fma(g, M, T)): M = 0 inside the window (T = bf16(silu(g))), M = 1/2
+# below it, M = 1 (g > 0) or 0 (g < 0) above it, and T = +-0 with the sign of
+# g outside it (tests/test_silu_table.py checks the whole rule against the
+# oracle on every bf16 value).
 SILU_LO = 0x3B00
-SILU_N = 2048
+SILU_N = 2046
+SILU_STRIDE = SILU_N + 2
 
 
 def silu_window_table() -> list[int]:
-    """binary32 bit patterns of bf16(silu(g)) over the window: entry i is the
-    pattern SILU_LO + i, entry SILU_N + i its negative."""
+    """The lookup table, SILU_STRIDE entries per sign (positive g first): entry
+    1 + i of a sign is the pattern SILU_LO + i, entry 0 the values below the
+    window, entry SILU_STRIDE - 1 those above it."""
     out = []
     for sign in (0, 0x8000):
+        below = (sign << 16) | 0x3F00  # T = +-0, M = 0.5
+        above = (sign << 16) | (0x0000 if sign else 0x3F80)  # T = +-0, M = 0 or 1
+        out.append(below)
         out.extend(silu_bf16(sign | (SILU_LO + i)) << 16 for i in range(SILU_N))
+        out.append(above)
     return out
 
 
 def write_silu_table() -> Path:
-    """csrc/_gen/silu_table.h: the window table of the SwiGLU epilogue."""
+    """csrc/_gen/silu_table.h: the lookup table of the SwiGLU epilogue."""
     GENERATED.mkdir(exist_ok=True)
     path = GENERATED / "silu_table.h"
     table = silu_window_table()
     rows = ["    " + ", ".join(f"0x{v:08x}u" for v in table[i:i + 8]) + "," for i in range(0, len(table), 8)]
     text = (
         "// Generated by vflash_amd/build.py (write_silu_table); not edited by hand.\n"
-        "// bf16(silu(g)) as binary32 bit patterns for 2^-9 <= |g| < 2^7: entry i is the bf16\n"
-        f"// pattern 0x{SILU_LO:04X} + i, entry {SILU_N} + i its negative.\n"
+        "// silu lookup entries: bf16(silu(g)) in the high half, a bf16 factor in the low\n"
+        f"// half; entry 1 + i of a sign is the pattern 0x{SILU_LO:04X} + i (2^-9 <= |g| <= 126.5),\n"
+        f"// entry 0 covers |g| below, entry {SILU_STRIDE - 1} above; the negative table starts at {SILU_STRIDE}.\n"
         "#pragma once\n#include <stdint.h>\n\nnamespace vfa {\n\n"
-        f"constexpr uint32_t kSiluLo = 0x{SILU_LO:04X}u, kSiluN = {SILU_N}u;\n\n"
-        f"__device__ const uint32_t kSiluTable[{2 * SILU_N}] __attribute__((aligned(16))) = {{\n"
+        f"constexpr uint32_t kSiluLo = 0x{SILU_LO:04X}u, kSiluN = {SILU_N}u, kSiluStride = {SILU_STRIDE}u;\n\n"
+        f"__device__ const uint32_t kSiluTable[{2 * SILU_STRIDE}] __attribute__((aligned(16))) = {{\n"
         + "\n".join(rows)
         + "\n};\n\n}  // namespace vfa\n"
     )

@@ -198,8 +198,12 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
   auto read_one = [&](int ja, int jw, auto ks, auto f) {
     const int cc = ks * 4 + fh * 2;
     const int o0 = (cc ^ fsw) << 4, o1 = ((cc + 1) ^ fsw) << 4;
-    const uint8_t* src = f < MB ? ring + a_slot(ja) + (wm * WM + fr) * BK + f * 32 * BK
-                                : ring + w_slot(jw) + (wn * WN + fr) * BK + (f - MB) * 32 * BK;
+    // Weight block f - MB of this wave: tile rows block_col(wn, f - MB) .. +31
+    // (SwiGLU tiles pair each value block with its gate block).
+    const uint8_t* src =
+        f < MB ? ring + a_slot(ja) + (wm * WM + fr) * BK + f * 32 * BK
+               : ring + w_slot(jw) + (wave_col<BN, WN, epi_swiglu(EPI)>(wn) + fr) * BK +
+                     block_off<BN, WN, epi_swiglu(EPI)>(f - MB) * BK;
     const v4i lo = *reinterpret_cast<const v4i*>(src + o0);
     const v4i hi = *reinterpret_cast<const v4i*>(src + o1);
     F[ks][f] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};

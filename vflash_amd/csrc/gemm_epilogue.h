@@ -59,6 +59,25 @@ __device__ __forceinline__ int64_t tile_column(const GemmParams& p, int64_t n0, 
   return n0 + c;
 }
 
+// Tile column of the first column of block nb of wave column wn (WN columns
+// per wave, NB blocks of 32).  SwiGLU tiles pair each value block with its
+// gate block inside one wave: block 2j is value block wn * NB/2 + j (tile
+// columns [0, BN/2)) and block 2j + 1 the matching gate block (BN/2 + the
+// same), so a lane holds the value and the gate of each of its outputs.
+template <int BN, int WN, bool SWIGLU>
+__device__ __forceinline__ int wave_col(int wn) {
+  return SWIGLU ? wn * (WN / 2) : wn * WN;
+}
+template <int BN, int WN, bool SWIGLU>
+constexpr int block_off(int nb) {
+  static_assert(!SWIGLU || (WN / 32) % 2 == 0, "value and gate blocks pair up");
+  return SWIGLU ? (nb & 1) * (BN / 2) + (nb / 2) * 32 : nb * 32;
+}
+template <int BN, int WN, bool SWIGLU>
+__device__ __forceinline__ int block_col(int wn, int nb) {
+  return wave_col<BN, WN, SWIGLU>(wn) + block_off<BN, WN, SWIGLU>(nb);
+}
+
 // The adapter branch of a wave's columns, from its first column `col`: the
 // offset of its t columns and its scale.  A wave's columns lie in one branch
 // (the launcher picks a tiling whose wave width divides lora_branch_cols).
@@ -88,10 +107,10 @@ __device__ __forceinline__ void lora_blocks(const GemmParams& p, int64_t m0, int
   constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
   constexpr int RS = 8;  // rank steps of 16: rank <= 128
   const int fr = lane & 31, fh = lane >> 5;
-  const LoraBranch br = lora_branch(p, tile_column<BN, SWIGLU>(p, n0, wn * WN));
+  const LoraBranch br = lora_branch(p, tile_column<BN, SWIGLU>(p, n0, block_col<BN, WN, SWIGLU>(wn, 0)));
   v8s bf[NB][RS], tf[MB][RS];
   static_for<NB>([&](auto nb) {
-    const int64_t nrow = tile_column<BN, SWIGLU>(p, n0, wn * WN + nb * 32) + fr;
+    const int64_t nrow = tile_column<BN, SWIGLU>(p, n0, block_col<BN, WN, SWIGLU>(wn, nb)) + fr;
     static_for<RS>([&](auto r) {
       bf[nb][r] = lora_frag(p.lora_b + nrow * p.ldb, p.rank, r, fh, nrow < p.n);
     });
@@ -119,25 +138,29 @@ __device__ __forceinline__ void lora_blocks(const GemmParams& p, int64_t m0, int
 // LDS bytes of the staged tile vectors: weight scales (or the one scalar),
 // activation row scales, bias.
 constexpr int VEC_LDS = 3 * 1024;
-// LDS bytes of the silu window table, which SwiGLU tiles stage after the vectors.
-constexpr int SILU_LDS = 2 * (int)kSiluN * 4;
+// LDS bytes of the silu lookup table, which SwiGLU tiles stage after the vectors.
+constexpr int SILU_LDS = 2 * (int)kSiluStride * 4;
 
-// bf16(silu(g)) as a binary32 value, for the bf16 pattern `bits` (low 16 bits)
-// of g: looked up in the window table `tab` (LDS) for 2^-9 <= |g| < 2^7, else
-// bf16(g / 2) below the window, g above it for g > 0 and g * 0 for g < 0 (-0,
-// or NaN for -inf and NaN).  Every bf16 input gives the binary32 formula
-// g / (1 + exp(-g)) of h3_fused_ops.py:205 with each step correctly rounded,
-// then rounded to bf16 (the window table is generated to that definition).
-__device__ __forceinline__ float silu_lookup(uint32_t bits, float g, const float* tab) {
-  const uint32_t a = bits & 0x7fffu;
-  const uint32_t i = a - kSiluLo;  // wraps around below the window
-  const uint32_t idx = min(i, kSiluN - 1u) | ((bits >> 4) & kSiluN);
-  const float t = tab[idx];
-  const float factor = a < kSiluLo ? 0.5f : ((bits & 0x8000u) ? 0.0f : 1.0f);
-  const float outside = g * factor;
-  // One rounding for both cases (table values are bf16 already), so that the
-  // choice stays a select rather than a branch around the conversion.
-  return round_bf16_wide(i < kSiluN ? t : outside);
+// bf16(silu(g)) as a binary32 value is silu_apply(g, silu_entry(g, tab)), for g
+// a bf16 value held as binary32 (low half zero) and `tab` the lookup table in
+// LDS; two steps, so a caller can have many table reads in flight.  The entry
+// is that of g's bf16 pattern for 2^-9 <= |g| <= 126.5, else the below- or
+// above-window entry of g's sign.
+// An entry holds T (high half) and a factor M (low half), both bf16, and the
+// result is bf16(fma(g, M, T)): T in the window; bf16(g / 2) below it; g above
+// it for g > 0 and g * 0 (-0, or NaN for -inf) for g < 0, T being a zero of g's
+// sign.  Every bf16 input gives the binary32 formula g / (1 + exp(-g)) of
+// h3_fused_ops.py:205 with each step correctly rounded, then rounded to bf16
+// (the table is generated to that definition).
+__device__ __forceinline__ uint32_t silu_entry(float g, const uint32_t* tab) {
+  const uint32_t gw = __float_as_uint(g);
+  const int a = (int)((gw >> 16) & 0x7fffu);
+  // Clamped to one entry below and one above the window.
+  const int c = min(max(a, (int)kSiluLo - 1), (int)(kSiluLo + kSiluN));
+  return tab[(gw >> 31) * kSiluStride + (uint32_t)(c - ((int)kSiluLo - 1))];
+}
+__device__ __forceinline__ float silu_apply(float g, uint32_t e) {
+  return round_bf16_wide(__builtin_fmaf(g, __uint_as_float(e << 16), __uint_as_float(e & 0xffff0000u)));
 }
 
 // Copy the scale and bias vectors of a BM x BN tile into LDS (vec_lds) with
@@ -192,14 +215,17 @@ __device__ __forceinline__ void stage_vectors(const GemmParams& p, int64_t m0, i
 //
 // Phase 1 (per wave, from the accumulators): a lane holds, for 32x32 block
 // (nb, mb) and register r, tile row mb*32 + (lane & 31) and tile column
-// nb*32 + 8*(r/4) + 4*(lane/32) + r%4 of its wave's sub-tile.  It applies the
-// scales, bias and the register-level epilogue (LoRA merge), rounds to
-// bf16 and writes the values into a BM x BN bf16 staging tile in LDS (16-byte
-// chunk c of row r stored in slot c ^ (r % chunks-per-row)).  Scale and bias
-// vectors are loaded once, before any store.
+// block_col(wn, nb) + 8*(r/4) + 4*(lane/32) + r%4.  It applies the scales,
+// bias and the register-level epilogue (LoRA merge), rounds to bf16 and
+// writes the values into a BM x BN bf16 staging tile in LDS (16-byte chunk c
+// of row r stored in slot c ^ (r % chunks-per-row)).  Scale and bias vectors
+// are loaded once, before any store.  SwiGLU tiles hold each output's value
+// and gate in one lane, so phase 1 forms h = bf16(value * bf16(silu(gate)))
+// there and stages the BM x BN/2 tile of h.
 // Phase 2 (whole workgroup): each thread moves 16-byte row chunks from LDS to
 // global memory with coalesced 16-byte stores, applying the gate-residual
-// epilogue there with coalesced residual loads.
+// epilogue there with coalesced residual loads (SwiGLU: and reducing the row
+// maxima of h).
 //
 // VEC: read the scale and bias vectors from the LDS copy `vec` made by
 // stage_vectors (true), or from global memory (false).
@@ -216,16 +242,19 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
                                               const v16f* lora_d = nullptr) {
   constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
   constexpr int NT = 64 * WGM * WGN;
-  constexpr int CH = BN / 8;  // 16-byte chunks per staged row
+  constexpr bool LORA = epi_lora(EPI), GATE = epi_gate(EPI), SWIGLU = epi_swiglu(EPI);
+  // Staged columns: the tile's, or the BN/2 outputs of a SwiGLU tile.
+  constexpr int SBN = SWIGLU ? BN / 2 : BN;
+  constexpr int CH = SBN / 8;  // 16-byte chunks per staged row
   // Chunk c of staged row r sits in slot c ^ (r % SWZ): every slot of a row
   // when CH is a power of two, else within its aligned group of 8 (CH = 24).
   constexpr int SWZ = (CH & (CH - 1)) == 0 ? CH : 8;
   static_assert(CH % SWZ == 0 && (SWZ & (SWZ - 1)) == 0, "swizzle stays inside the row");
-  constexpr int PITCH = BN * 2;
+  constexpr int PITCH = SBN * 2;
   const int lane = tid & 63, fr = lane & 31, fh = lane >> 5;
-  constexpr bool LORA = epi_lora(EPI), GATE = epi_gate(EPI), SWIGLU = epi_swiglu(EPI);
   const LoraBranch br =
-      LORA ? lora_branch(p, tile_column<BN, SWIGLU>(p, n0, wn * WN)) : LoraBranch{0, 1.0f};
+      LORA ? lora_branch(p, tile_column<BN, SWIGLU>(p, n0, block_col<BN, WN, SWIGLU>(wn, 0)))
+           : LoraBranch{0, 1.0f};
   const float* __restrict__ sa_p = p.sa;
   const float* __restrict__ sw_p = p.sw;
   const uint16_t* __restrict__ bias_p = p.bias;
@@ -244,6 +273,44 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
   });
   const float sw0 = VEC && SW_SCALAR ? reinterpret_cast<const float*>(vec)[0] : 0.0f;
 
+  // The LoRA delta of block (nb, mb) as bf16 values held in binary32: the
+  // products computed ahead of the main loop, or B[n, :] . t[m, :] on bf16
+  // MFMA (binary32 accumulation) with the operands of every rank step (rank <=
+  // 128) loaded before the first MFMA, so a block waits for one memory round
+  // trip, not one per step; then bf16(t . B^T) and the optional bf16(delta *
+  // scale) and bf16(delta * strength) steps, for the block's 16 values at once
+  // (two uniform branches per block).
+  auto lora_delta = [&](auto nb, auto mb) {
+    v16f d = v16f{};
+    if constexpr (LORA) {
+      if (lora_d) {
+        d = lora_d[nb * MB + mb];
+      } else {
+        const int64_t m = m0 + wm * WM + mb * 32 + fr;
+        const int64_t nrow = tile_column<BN, SWIGLU>(p, n0, block_col<BN, WN, SWIGLU>(wn, nb)) + fr;
+        const bool nok = nrow < p.n, mvalid = m < p.m;
+        v8s bfr[8], tfr[8];
+        static_for<8>([&](auto st) {
+          bfr[st] = lora_frag(p.lora_b + nrow * p.ldb, p.rank, st, fh, nok);
+          tfr[st] = lora_frag(p.lora_t + m * p.ldt + br.toff, p.rank, st, fh, mvalid);
+        });
+        static_for<8>([&](auto st) {
+          if (st * 16 < p.rank)
+            d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, bfr[st]),
+                                                        __builtin_bit_cast(v8bf, tfr[st]), d, 0, 0,
+                                                        0);
+        });
+      }
+      auto round_pairs = [&](float f) {
+        static_for<16>([&](auto i) { d[(int)i] = round_bf16_wide(d[(int)i] * f); });
+      };
+      round_pairs(1.0f);
+      if (br.scale != 1.0f) round_pairs(br.scale);
+      if (p.lora_strength != 1.0f) round_pairs(p.lora_strength);
+    }
+    return d;
+  };
+
   // Phase 1, column-block major: the scale and bias of one 32-column block (4
   // columns per g for this lane) are live while its MB row blocks are written.
   // Two copies (with and without bias) keep the bias test out of the loop.
@@ -252,25 +319,35 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
     // compiler knows the staging writes below may alias them, so a read placed
     // after a write waits for that write, and reads issued block by block would
     // each pay a full LDS round trip.
-    v4f s4r[VEC ? NB : 1][4];
-    uint2 b4r[VEC ? NB : 1][4];
-    if constexpr (VEC) {
+    // (SwiGLU tiles, whose phase 1 holds more registers, read them one pair of
+    // blocks at a time instead.)
+    constexpr int PRE_NB = VEC && !SWIGLU ? NB : 1;
+    v4f s4r[PRE_NB][4];
+    uint2 b4r[PRE_NB][4];
+    if constexpr (VEC && !SWIGLU) {
       static_for<NB>([&](auto nb) {
         static_for<4>([&](auto g) {
-          const int col = wn * WN + nb * 32 + g * 8 + fh * 4;
+          const int col = block_col<BN, WN, SWIGLU>(wn, nb) + g * 8 + fh * 4;
           s4r[nb][g] = *reinterpret_cast<const v4f*>(vec + col * 4);
           b4r[nb][g] = has_bias ? *reinterpret_cast<const uint2*>(vec + 2048 + col * 2)
                                 : make_uint2(0u, 0u);
         });
       });
     }
-    static_for<NB>([&](auto nb) {
-      float sv[4][4], bv[4][4];
+    // Scale and bias of the 16 columns block nb holds in this lane.
+    auto block_vectors = [&](auto nb, float (&sv)[4][4], float (&bv)[4][4]) {
       static_for<4>([&](auto g) {
-        const int col = wn * WN + nb * 32 + g * 8 + fh * 4;  // tile column of value i = 0
+        const int col = block_col<BN, WN, SWIGLU>(wn, nb) + g * 8 + fh * 4;  // value i = 0
         if constexpr (VEC) {
-          const v4f s4 = s4r[nb][g];
-          const uint2 b4 = b4r[nb][g];
+          v4f s4;
+          uint2 b4;
+          if constexpr (SWIGLU) {
+            s4 = *reinterpret_cast<const v4f*>(vec + col * 4);
+            b4 = has_bias ? *reinterpret_cast<const uint2*>(vec + 2048 + col * 2) : make_uint2(0u, 0u);
+          } else {
+            s4 = s4r[SWIGLU ? 0 : (int)nb][g];
+            b4 = b4r[SWIGLU ? 0 : (int)nb][g];
+          }
           static_for<4>([&](auto i) {
             sv[g][i] = SW_SCALAR ? sw0 : s4[(int)i];
             const uint32_t bw = i < 2 ? b4.x : b4.y;
@@ -285,42 +362,68 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
           });
         }
       });
+    };
+    // The epilogue value of register i of a block before its last bf16
+    // rounding: bf16(acc * sa * sw) + bias, then bf16(.) + delta where present
+    // (the reference's roundings, in order).
+    auto value = [&](float a, float sm, float sc, float b, float dl) {
+      float y = a * sm * sc;
+      if constexpr (has_bias) y = round_bf16_wide(y) + b;
+      if constexpr (LORA) y = round_bf16_wide(y) + dl;
+      return y;
+    };
+    if constexpr (SWIGLU) {
+      // Value block 2j and gate block 2j + 1 hold the same outputs.
+      const uint32_t* const silu_tab = reinterpret_cast<const uint32_t*>(vec + VEC_LDS);
+      static_for<NB / 2>([&](auto j) {
+        constexpr int vb = 2 * j, gb = 2 * j + 1;
+        float svv[4][4], bvv[4][4], svg[4][4], bvg[4][4];
+        block_vectors(std::integral_constant<int, vb>{}, svv, bvv);
+        block_vectors(std::integral_constant<int, gb>{}, svg, bvg);
+        static_for<MB>([&](auto mb) {
+          const int row = wm * WM + mb * 32 + fr;  // tile row
+          const v16f dv = lora_delta(std::integral_constant<int, vb>{}, mb);
+          const v16f dg = lora_delta(std::integral_constant<int, gb>{}, mb);
+          // Eight outputs at a time: their gates and table reads first, then
+          // the values while the reads are in flight (scheduling barriers
+          // keep the groups apart).
+          static_for<2>([&](auto half) {
+            float gt[8], vl[8];
+            uint32_t e[8];
+            static_for<8>([&](auto t) {
+              constexpr int i = 8 * half + t, g = i / 4, k = i % 4;
+              gt[t] = round_bf16_wide(value(acc[gb][mb][i], sam[mb], svg[g][k], bvg[g][k], dg[i]));
+            });
+            static_for<8>([&](auto t) { e[t] = silu_entry(gt[t], silu_tab); });
+            __builtin_amdgcn_sched_barrier(0);
+            static_for<8>([&](auto t) {
+              constexpr int i = 8 * half + t, g = i / 4, k = i % 4;
+              vl[t] = round_bf16_wide(value(acc[vb][mb][i], sam[mb], svv[g][k], bvv[g][k], dv[i]));
+            });
+            __builtin_amdgcn_sched_barrier(0);
+            static_for<2>([&](auto gg) {
+              constexpr int g = 2 * half + gg;
+              uint32_t w[2];
+              static_for<2>([&](auto h) {
+                constexpr int t0 = 4 * gg + 2 * h, t1 = t0 + 1;
+                w[h] = pack_bf16x2(vl[t0] * silu_apply(gt[t0], e[t0]), vl[t1] * silu_apply(gt[t1], e[t1]));
+              });
+              // Output chunk of these 4 columns (the value block's tile column / 8).
+              const int c = (block_col<BN, WN, SWIGLU>(wn, vb) + g * 8) / 8;
+              *reinterpret_cast<uint2*>(stage + row * PITCH + ((c ^ (row & (SWZ - 1))) << 4) + fh * 8) =
+                  make_uint2(w[0], w[1]);
+            });
+          });
+        });
+      });
+      return;
+    }
+    static_for<NB>([&](auto nb) {
+      float sv[4][4], bv[4][4];
+      block_vectors(nb, sv, bv);
       static_for<MB>([&](auto mb) {
         const int row = wm * WM + mb * 32 + fr;  // tile row
-        const int64_t m = m0 + row;
-        const bool mvalid = m < p.m;
-        v16f d = v16f{};
-        if (LORA && lora_d) {
-          d = lora_d[nb * MB + mb];
-        } else if constexpr (LORA) {
-          // delta block = B[n, :] . t[m, :] on bf16 MFMA, binary32 accumulate.  The
-          // operands of every rank step (rank <= 128) are loaded before the first
-          // MFMA, so a block waits for one memory round trip, not one per step.
-          const int64_t nrow = tile_column<BN, SWIGLU>(p, n0, wn * WN + nb * 32) + fr;
-          const bool nok = nrow < p.n;
-          v8s bfr[8], tfr[8];
-          static_for<8>([&](auto st) {
-            bfr[st] = lora_frag(p.lora_b + nrow * p.ldb, p.rank, st, fh, nok);
-            tfr[st] = lora_frag(p.lora_t + m * p.ldt + br.toff, p.rank, st, fh, mvalid);
-          });
-          static_for<8>([&](auto st) {
-            if (st * 16 < p.rank)
-              d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, bfr[st]),
-                                                          __builtin_bit_cast(v8bf, tfr[st]), d, 0,
-                                                          0, 0);
-          });
-        }
-        if constexpr (LORA) {
-          // delta = bf16(t . B^T), then the optional bf16(delta * scale) and
-          // bf16(delta * strength) steps, for the block's 16 values at once (two
-          // uniform branches per block); d then holds bf16 values as binary32.
-          auto round_pairs = [&](float f) {
-            static_for<16>([&](auto i) { d[(int)i] = round_bf16_wide(d[(int)i] * f); });
-          };
-          round_pairs(1.0f);
-          if (br.scale != 1.0f) round_pairs(br.scale);
-          if (p.lora_strength != 1.0f) round_pairs(p.lora_strength);
-        }
+        const v16f d = lora_delta(nb, mb);
         static_for<4>([&](auto g) {
           uint32_t w[2];
           // Output pairs: a bf16 rounding whose result is used again is one
@@ -340,7 +443,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
             }
             w[h] = pack_bf16x2(y0, y1);
           });
-          const int c = (wn * WN + nb * 32 + g * 8) / 8;  // 16-byte chunk of the row
+          const int c = (block_col<BN, WN, SWIGLU>(wn, nb) + g * 8) / 8;  // 16-byte chunk of the row
           *reinterpret_cast<uint2*>(stage + row * PITCH + ((c ^ (row & (SWZ - 1))) << 4) + fh * 8) =
               make_uint2(w[0], w[1]);
         });
@@ -355,24 +458,20 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
   __syncthreads();
 
   if constexpr (SWIGLU) {
-    // Phase 2 of the SwiGLU tile: value chunk c and gate chunk c + CH/2 of a
-    // row give 8 outputs h = bf16(value * bf16(silu(gate))) (the eager bf16
-    // order of h3_fused_ops.py:184-224); the 16 threads of a row also reduce
-    // max |h| over the tile's 128 output columns for the requantization.
-    constexpr int CHO = CH / 2;   // output chunks per row
-    constexpr int RPO = NT / CHO; // rows per pass
-    static_assert(CHO == 16 && BM % RPO == 0, "one 16-lane group per row");
-    const int c = tid % CHO, r0 = tid / CHO;
+    // Phase 2 of the SwiGLU tile: 16 threads per row store its 128 outputs of
+    // h (8 per thread) and reduce max |h| over them for the requantization.
+    constexpr int RPO = NT / CH;  // rows per pass
+    static_assert(CH == 16 && BM % RPO == 0, "one 16-lane group per row");
+    const int c = tid % CH, r0 = tid / CH;
     const int64_t n = n0 + c * 8;
     const int rows = (int)min((int64_t)BM, p.m - m0);
     const int parts = (int)((p.half_n + BN / 2 - 1) / (BN / 2));
     const int part = (int)(n0 / (BN / 2));
     static_assert(VEC, "the silu table is staged with the vectors");
-    const float* const silu_tab = reinterpret_cast<const float*>(vec + VEC_LDS);
-    // The swizzle of row r0 + it * RPO repeats every two passes: two LDS
-    // offsets per half serve every pass.  The chunks of a batch of rows are
-    // read before any is used, so the LDS latency is paid once per batch.
-    static_assert((2 * RPO) % SWZ == 0, "the swizzle repeats every two passes");
+    // The swizzle of row r0 + it * RPO repeats every four passes: four LDS
+    // offsets serve every pass.  The chunks of a batch of rows are read before
+    // any is used, so the LDS latency is paid once per batch.
+    static_assert((4 * RPO) % SWZ == 0, "the swizzle repeats every four passes");
     constexpr int PASSES = BM / RPO, BATCH = PASSES < 8 ? PASSES : 8;
     // Output row r0 + it * RPO: one row step per pass for h and for the maxima.
     uint16_t* const out0 = p.out + (m0 + r0) * p.ldo + n;
@@ -380,42 +479,29 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
     float* const amax0 = p.amax_part + (m0 + r0) * parts + part;
     const int64_t astep = (int64_t)RPO * parts;
     const bool full = rows == BM;
-    int vofs[2], gofs[2];
+    int ofs[4];
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int rs = (r0 + k * RPO) & (SWZ - 1);
-      vofs[k] = r0 * PITCH + ((c ^ rs) << 4);
-      gofs[k] = r0 * PITCH + (((c + CHO) ^ rs) << 4);
-    }
+    for (int k = 0; k < 4; ++k) ofs[k] = r0 * PITCH + ((c ^ ((r0 + k * RPO) & (SWZ - 1))) << 4);
 #pragma unroll
     for (int it0 = 0; it0 < PASSES; it0 += BATCH) {
-      v4i vv[BATCH], gg[BATCH];
+      v4i hh[BATCH];
 #pragma unroll
       for (int j = 0; j < BATCH; ++j) {
         const int it = it0 + j;
-        vv[j] = *reinterpret_cast<const v4i*>(stage + vofs[it & 1] + it * RPO * PITCH);
-        gg[j] = *reinterpret_cast<const v4i*>(stage + gofs[it & 1] + it * RPO * PITCH);
+        hh[j] = *reinterpret_cast<const v4i*>(stage + ofs[it & 3] + it * RPO * PITCH);
       }
 #pragma unroll
       for (int j = 0; j < BATCH; ++j) {
-        const int row = r0 + (it0 + j) * RPO;
-        v4i h;
+        const int it = it0 + j;
+        const int row = r0 + it * RPO;
         uint32_t amax_pk = 0u;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t vw = (uint32_t)vv[j][q], gw = (uint32_t)gg[j][q];
-          const float s0 = silu_lookup(gw, bf16_lo(gw), silu_tab);
-          const float s1 = silu_lookup(gw >> 16, bf16_hi(gw), silu_tab);
-          const uint32_t hw = pack_bf16x2(bf16_lo(vw) * s0, bf16_hi(vw) * s1);
-          amax_pk = abs_max_pk(amax_pk, hw);
-          h[q] = (int)hw;
-        }
+        for (int q = 0; q < 4; ++q) amax_pk = abs_max_pk(amax_pk, (uint32_t)hh[j][q]);
         // Maximum over the 16 lanes of the 128-column group (one DPP row),
         // NaN propagated: the bit patterns of |h| compare as unsigned integers.
         const float amax = __uint_as_float(row16_max_u32(__float_as_uint(abs_max_value(amax_pk))));
-        const int it = it0 + j;
         if (full || row < rows) {
-          if (n < p.half_n) *reinterpret_cast<v4i*>(out0 + it * ostep) = h;
+          if (n < p.half_n) *reinterpret_cast<v4i*>(out0 + it * ostep) = hh[j];
           if (c == 0) amax0[it * astep] = amax;
         }
       }
