@@ -615,6 +615,57 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
       for (int k = 0; k < 4; ++k) lofs[k] = r0 * PITCH + ((c ^ ((r0 + k * RPP) & (SWZ - 1))) << 4);
       uint16_t* const dst0 = base + (m0 + r0) * p.ldo;
       const int64_t dstep = (int64_t)RPP * p.ldo;
+      if constexpr (GATE) {
+        // Gate-residual: the residual and gate chunks of batch b + 1 are
+        // loaded before batch b is combined and stored, so their latency
+        // overlaps that work.  A gate of one row (no index) is loaded once.
+        constexpr int NBATCH = (PASSES + BATCH - 1) / BATCH;
+        auto run = [&](auto bcast) {
+          v4i gate0 = v4i{};
+          if constexpr (bcast) gate0 = *reinterpret_cast<const v4i*>(p.gate + n);
+          GateIn in[2][BATCH];
+          auto load = [&](auto b) {
+            static_for<BATCH>([&](auto j) {
+              constexpr int it = b * BATCH + j;
+              const int row = r0 + it * RPP;
+              if constexpr (it < PASSES) {
+                if (PASSES * RPP == BM || row < BM) {
+                  if constexpr (bcast) {
+                    in[b & 1][j].res = *reinterpret_cast<const v4i*>(p.residual + (m0 + row) * p.ldr + n);
+                    in[b & 1][j].gate = gate0;
+                  } else {
+                    in[b & 1][j] = gate_in(row, tok, std::true_type{});
+                  }
+                }
+                if constexpr (!bcast) next_tok();
+              }
+            });
+          };
+          load(std::integral_constant<int, 0>{});
+          static_for<NBATCH>([&](auto b) {
+            v4i v[BATCH];
+            static_for<BATCH>([&](auto j) {
+              constexpr int it = b * BATCH + j;
+              if constexpr (it < PASSES)
+                v[j] = *reinterpret_cast<const v4i*>(stage + lofs[it & 3] + it * RPP * PITCH);
+            });
+            if constexpr (b + 1 < NBATCH) load(std::integral_constant<int, b + 1>{});
+            static_for<BATCH>([&](auto j) {
+              constexpr int it = b * BATCH + j;
+              const int row = r0 + it * RPP;
+              if constexpr (it < PASSES) {
+                if (PASSES * RPP == BM || row < BM)
+                  store(gate_apply(v[j], in[b & 1][j]), dst0 + it * dstep, vec_out);
+              }
+            });
+          });
+        };
+        if (tokens == 1 && !p.gate_index)
+          run(std::true_type{});
+        else
+          run(std::false_type{});
+        return;
+      }
 #pragma unroll
       for (int it0 = 0; it0 < PASSES; it0 += BATCH) {
         v4i v[BATCH];
