@@ -172,8 +172,10 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
 
   v16f acc[NB][MB];
   static_for<NB>([&](auto i) { static_for<MB>([&](auto jj) { acc[i][jj] = v16f{}; }); });
-  // Block scales of the current 16-K block as binary16 pairs: steps 2b and
-  // 2b + 1 of a half share block b, so each is converted once per two steps.
+  // Block scales of the current half as binary16: a lane's two 16-K blocks of
+  // the half (bytes 2 fh and 2 fh + 1 of the row's scale word), converted by
+  // one instruction at the half's first step; step v multiplies by element
+  // v / 2, broadcast to both halves of the packed multiply.
   v2h scw[NB], sca[A4 ? MB : 1];
   // Binary16 operands of MFMA step v (0..3) of a half held in r.
   struct Ops {
@@ -181,17 +183,18 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
   };
   auto convert = [&](const Raw& r, auto v) {
     Ops o;
-    // E4M3 block scale (byte 2*fh + v/2 of the row's scale word), exact in binary16.
+    // E4M3 block scales (bytes 2*fh, 2*fh + 1 of the row's scale word), exact in binary16.
     auto scale_pair = [&](uint32_t sword) {
-      const uint32_t sb = (sword >> (16 * fh + 8 * (v / 2))) & 0xffu;
-      return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(sb | (sb << 8), 1.0f, false);
+      return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(sword >> (16 * fh), 1.0f, false);
     };
-    if constexpr (v % 2 == 0) {
+    if constexpr (v == 0) {
       static_for<NB>([&](auto nb) { scw[nb] = scale_pair(r.s[nb]); });
       if constexpr (A4) static_for<MB>([&](auto mb) { sca[mb] = scale_pair(r.as[mb]); });
     }
-    // Eight E2M1 values of packed word d times their block scale sc, exact in binary16.
-    auto fp4x8 = [&](uint32_t d, v2h sc) {
+    // Eight E2M1 values of packed word d times their block scale (element v / 2
+    // of sc2), exact in binary16.
+    auto fp4x8 = [&](uint32_t d, v2h sc2) {
+      const v2h sc = v2h{sc2[v / 2], sc2[v / 2]};
       const v2h y0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.0f, 0) * sc;
       const v2h y1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.0f, 1) * sc;
       const v2h y2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.0f, 2) * sc;
