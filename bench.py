@@ -206,27 +206,59 @@ class EventTimer:
 
     The kernels run on torch's current stream (the C-ABI is handed
     ``torch.cuda.current_stream()``), so events recorded on that stream bracket
-    exactly one launch each.
+    exactly one launch each.  The events are created before the timed steps
+    (``n`` pairs), so the timed region only records them.
     """
 
-    def __init__(self):
-        self.pairs = []
+    def __init__(self, n=0):
+        import torch
+
+        self.stream = torch.cuda.current_stream()
+        self.pool = [self._pair() for _ in range(n)]
+        self.used = 0
+
+    @staticmethod
+    def _pair():
+        import torch
+
+        return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
     def start(self):
-        import torch
-
-        s = torch.cuda.Event(enable_timing=True)
-        e = torch.cuda.Event(enable_timing=True)
-        s.record(torch.cuda.current_stream())
-        self.pairs.append((s, e))
+        if self.used == len(self.pool):
+            self.pool.append(self._pair())
+        self.pool[self.used][0].record(self.stream)
 
     def stop(self):
-        import torch
-
-        self.pairs[-1][1].record(torch.cuda.current_stream())
+        self.pool[self.used][1].record(self.stream)
+        self.used += 1
 
     def times_ms(self):
-        return [s.elapsed_time(e) for s, e in self.pairs]
+        return [s.elapsed_time(e) for s, e in self.pool[:self.used]]
+
+
+class _NullScope:
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False
+
+
+class _TimedScope:
+    __slots__ = ("timer",)
+
+    def __init__(self, timer):
+        self.timer = timer
+
+    def __enter__(self):
+        self.timer.start()
+
+    def __exit__(self, *exc):
+        self.timer.stop()
+        return False
+
+
+_NULL_SCOPE = _NullScope()
 
 
 class ScopeTimer:
@@ -242,19 +274,10 @@ class ScopeTimer:
         self.timer = timer
 
     def __call__(self, name):
-        from contextlib import contextmanager, nullcontext
-
         if name != "linear.fp8_gemm" or self.timer is None:
-            return nullcontext()
+            return _NULL_SCOPE
         timer, self.timer = self.timer, None
-
-        @contextmanager
-        def scope():
-            timer.start()
-            yield
-            timer.stop()
-
-        return scope()
+        return _TimedScope(timer)
 
 
 class Workload:
@@ -737,7 +760,7 @@ def main():
     _lib.library()
 
     w = make_workload(args, dev)
-    timer = EventTimer()
+    timer = EventTimer(args.steps)
     # Settle: the step, untimed, until the device has run it for settle_ms (the
     # clocks of a fresh process ramp over its first tens of milliseconds).
     settled = 0.0
@@ -765,7 +788,7 @@ def main():
     if w.launch_bound:
         # Hold the stream with a spin kernel while the host enqueues every step,
         # then time the same steps on the device with events around the run.
-        timer = EventTimer()
+        timer = EventTimer(args.steps)
         torch.cuda._sleep(100_000_000)
         first = torch.cuda.Event(enable_timing=True)
         last = torch.cuda.Event(enable_timing=True)

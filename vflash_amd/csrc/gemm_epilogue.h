@@ -606,8 +606,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
       // every four passes, so four LDS offsets and one output row step serve
       // every pass.  With CH = 24 (26 passes of 10 rows) the last pass reaches
       // rows up to 259: those past BM are read from LDS (at most 100 KB into the
-      // 112 KB ring) but neither loaded from global memory nor stored; the
-      // batch's passes past the last (26..31) read nothing.
+      // 136 KB ring, below the vectors at 112 KB) but neither loaded from global
+      // memory nor stored; the batch's passes past the last (26..31) read nothing.
       static_assert((4 * RPP) % SWZ == 0, "the swizzle repeats every four passes");
       constexpr int BATCH = PASSES < 8 ? PASSES : 8;
       int lofs[4];
