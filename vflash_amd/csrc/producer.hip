@@ -25,8 +25,10 @@
 
 namespace vfa {
 
-// Norm and modulation of the two bf16 of one 32-bit word (low element first),
-// every rounding done for both at once; returns y as a packed bf16 pair.
+// Norm and modulation of the two bf16 of one 32-bit word (low element first);
+// returns y as a packed bf16 pair.  A bf16 rounding whose result is used again
+// is one conversion that leaves bf16(v) widened in the register
+// (round_bf16_wide); the last one packs the pair.
 template <bool HAS_W>
 __device__ __forceinline__ uint32_t modulate2(float xl, float xh, uint32_t wv, uint32_t sv,
                                               uint32_t hv, float rstd) {
@@ -35,10 +37,9 @@ __device__ __forceinline__ uint32_t modulate2(float xl, float xh, uint32_t wv, u
     nl *= bf16_lo(wv);
     nh *= bf16_hi(wv);
   }
-  const uint32_t n = pack_bf16x2(nl, nh);
-  const uint32_t s1 = pack_bf16x2(1.0f + bf16_lo(sv), 1.0f + bf16_hi(sv));
-  const uint32_t a = pack_bf16x2(bf16_lo(n) * bf16_lo(s1), bf16_hi(n) * bf16_hi(s1));
-  return pack_bf16x2(bf16_lo(a) + bf16_lo(hv), bf16_hi(a) + bf16_hi(hv));
+  const float al = round_bf16_wide(round_bf16_wide(nl) * round_bf16_wide(1.0f + bf16_lo(sv)));
+  const float ah = round_bf16_wide(round_bf16_wide(nh) * round_bf16_wide(1.0f + bf16_hi(sv)));
+  return pack_bf16x2(al + bf16_lo(hv), ah + bf16_hi(hv));
 }
 
 // k % 8 == 0; x, norm_w, scale, shift, values 16-byte aligned with row strides
