@@ -59,11 +59,12 @@ __device__ __forceinline__ int64_t tile_column(const GemmParams& p, int64_t n0, 
   return n0 + c;
 }
 
-// Tile column of the first column of block nb of wave column wn (WN columns
-// per wave, NB blocks of 32).  SwiGLU tiles pair each value block with its
-// gate block inside one wave: block 2j is value block wn * NB/2 + j (tile
-// columns [0, BN/2)) and block 2j + 1 the matching gate block (BN/2 + the
-// same), so a lane holds the value and the gate of each of its outputs.
+// block_col(wn, nb) = wave_col(wn) + block_off(nb): the tile column of the
+// first column of block nb of wave column wn (WN columns per wave, NB blocks
+// of 32).  SwiGLU tiles pair each value block with its gate block inside one
+// wave: block 2j is value block wn * NB/2 + j (tile columns [0, BN/2)) and
+// block 2j + 1 the matching gate block (BN/2 + the same), so a lane holds the
+// value and the gate of each of its outputs.
 template <int BN, int WN, bool SWIGLU>
 __device__ __forceinline__ int wave_col(int wn) {
   return SWIGLU ? wn * (WN / 2) : wn * WN;
@@ -319,8 +320,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
     // compiler knows the staging writes below may alias them, so a read placed
     // after a write waits for that write, and reads issued block by block would
     // each pay a full LDS round trip.
-    // (SwiGLU tiles, whose phase 1 holds more registers, read them one pair of
-    // blocks at a time instead.)
+    // (SwiGLU tiles, whose phase 1 holds more registers, read them block by
+    // block instead, for one value/gate pair of blocks at a time.)
     constexpr int PRE_NB = VEC && !SWIGLU ? NB : 1;
     v4f s4r[PRE_NB][4];
     uint2 b4r[PRE_NB][4];
@@ -345,8 +346,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
             s4 = *reinterpret_cast<const v4f*>(vec + col * 4);
             b4 = has_bias ? *reinterpret_cast<const uint2*>(vec + 2048 + col * 2) : make_uint2(0u, 0u);
           } else {
-            s4 = s4r[SWIGLU ? 0 : (int)nb][g];
-            b4 = b4r[SWIGLU ? 0 : (int)nb][g];
+            s4 = s4r[nb][g];
+            b4 = b4r[nb][g];
           }
           static_for<4>([&](auto i) {
             sv[g][i] = SW_SCALAR ? sw0 : s4[(int)i];
