@@ -64,15 +64,22 @@ def test_linear_bias_random_shape(dev, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", shapes(6, 8))
-def test_gate_residual_random_shape(dev, m, n, k):
+@pytest.mark.parametrize("gate_form", ["per_row", "broadcast", "one_row"])
+def test_gate_residual_random_shape(dev, m, n, k, gate_form):
+    # Per-row gates [m, n], and the one-row forms [n] and [1, n] (loaded once
+    # per thread in whole tiles).
     x, cw, sw, bias = operands(dev, m, n, k, 3 * m + n + k)
     g = torch.Generator().manual_seed(m + 2 * n)
     res = torch.randn((m, n), generator=g).to(torch.bfloat16).to(dev)
-    gate = torch.rand((m, n), generator=g).to(torch.bfloat16).to(dev)
+    rows = {"per_row": m, "broadcast": 1, "one_row": 1}[gate_form]
+    gate = torch.rand((rows, n), generator=g).to(torch.bfloat16).to(dev)
+    if gate_form == "broadcast":
+        gate = gate[0]
 
     def run(lo, hi):
         c, s = kernels.quantize_rows(x[lo:hi])
-        return kernels.fp8_gemm_gate_residual(c, s, cw, sw, hi - lo, gate[lo:hi], res[lo:hi], bias)
+        gt = gate[lo:hi] if gate_form == "per_row" else gate
+        return kernels.fp8_gemm_gate_residual(c, s, cw, sw, hi - lo, gt, res[lo:hi], bias)
 
     out = split_equal(run, m, max(1, m // 2))
     codes, sa = T.quantize_rows(x)
@@ -82,7 +89,8 @@ def test_gate_residual_random_shape(dev, m, n, k):
     c, s = kernels.quantize_rows(x)
     y_k = kernels.fp8_gemm(c, s, cw, sw, m, bias)
     rel_check_device(y_k, y)
-    assert torch.equal(out, T.gate_residual(res, gate, y_k).to(torch.bfloat16))
+    full_gate = gate.reshape(-1, n).expand(m, n)
+    assert torch.equal(out, T.gate_residual(res, full_gate, y_k).to(torch.bfloat16))
 
 
 @pytest.mark.parametrize("m,n,k", shapes(7, 8))
