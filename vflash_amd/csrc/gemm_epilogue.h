@@ -601,9 +601,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
   auto pass = [&](auto vec_out) {
     if (rows == BM && (!GATE || vec_in)) {
       // A whole tile (with vector residual and gate loads for the gate-residual): the
-      // chunks of BATCH rows (and their residual and gate chunks) are loaded
-      // before any is stored, so each latency is paid once
-      // per batch, not once per row.  The swizzle of row r0 + it * RPP repeats
+      // chunks of BATCH rows are read from LDS before any is stored, so each
+      // latency is paid once per batch, not once per row.  The swizzle of row r0 + it * RPP repeats
       // every four passes, so four LDS offsets and one output row step serve
       // every pass.  With CH = 24 (26 passes of 10 rows) the last pass reaches
       // rows up to 259: those past BM are read from LDS (at most 100 KB into the
@@ -665,32 +664,21 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
           run(std::true_type{});
         else
           run(std::false_type{});
-        return;
-      }
+      } else {
 #pragma unroll
-      for (int it0 = 0; it0 < PASSES; it0 += BATCH) {
-        v4i v[BATCH];
-        GateIn in[BATCH];
+        for (int it0 = 0; it0 < PASSES; it0 += BATCH) {
+          v4i v[BATCH];
 #pragma unroll
-        for (int j = 0; j < BATCH; ++j) {
-          const int it = it0 + j;
-          const int row = r0 + it * RPP;
-          if (it < PASSES)  // a constant: the loop is unrolled
-            v[j] = *reinterpret_cast<const v4i*>(stage + lofs[it & 3] + it * RPP * PITCH);
-          if constexpr (GATE) {
-            if (it < PASSES && (PASSES * RPP == BM || row < BM))
-              in[j] = gate_in(row, tok, std::true_type{});
-            next_tok();
+          for (int j = 0; j < BATCH; ++j) {
+            const int it = it0 + j;
+            if (it < PASSES)  // a constant: the loop is unrolled
+              v[j] = *reinterpret_cast<const v4i*>(stage + lofs[it & 3] + it * RPP * PITCH);
           }
-        }
 #pragma unroll
-        for (int j = 0; j < BATCH; ++j) {
-          const int it = it0 + j;
-          const int row = r0 + it * RPP;
-          if (it < PASSES && (PASSES * RPP == BM || row < BM)) {
-            v4i o = v[j];
-            if constexpr (GATE) o = gate_apply(o, in[j]);
-            store(o, dst0 + it * dstep, vec_out);
+          for (int j = 0; j < BATCH; ++j) {
+            const int it = it0 + j;
+            const int row = r0 + it * RPP;
+            if (it < PASSES && (PASSES * RPP == BM || row < BM)) store(v[j], dst0 + it * dstep, vec_out);
           }
         }
       }
