@@ -62,6 +62,11 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
   constexpr int BK = 128, WGM = 2, WGN = 2;
   constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
   constexpr bool SPLIT = NS == SPLIT_RING;
+  // Split-ring tiles with the plain or gate-residual epilogue issue their last
+  // K substep's MFMAs from the epilogue, under its phase-1 work; the adapter
+  // and SwiGLU epilogues hold too many registers for the fragments to stay
+  // live through them.
+  constexpr bool EPI_OVERLAP = SPLIT && !epi_lora(EPI) && !epi_swiglu(EPI);
   constexpr int HA = BM * BK;              // activation rows of one stage
   constexpr int HW = BN * BK;              // weight rows of one stage
   constexpr int SLOT = (BM + BN) * BK;     // one stage: activation rows, then weight rows
@@ -336,6 +341,16 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
       static_for<(MB + NB > Q ? MB + NB - Q : 0)>([&](auto i) {
         read_one(ja, jw, I1{}, std::integral_constant<int, Q + i>{});
       });
+      if constexpr (last && EPI_OVERLAP) {
+        // The last stage's substep-1 MFMAs are issued by the epilogue, between
+        // its blocks.  Every DMA (the vectors included) has landed and the
+        // ring is read: the epilogue may stage its output there.
+        wait_vmcnt<0, true>();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        return;
+      }
       // Stage kt+1 has landed for every wave (the weight DMAs of stage kt+2 may
       // still be in flight); stage kt is fully read.
       wait_vmcnt<DMA_W, true>();
@@ -386,13 +401,26 @@ __device__ __forceinline__ void pipe_tile(const GemmParams& p, int tm, int tn, u
   } else {
     run(std::false_type{});
   }
-  wait_vmcnt<0, true>();  // every DMA has landed before the ring is reused
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-  // The thread index after the loop, recomputed rather than held through it.
-  gemm_epilogue<BM, BN, WGM, WGN, EPI, true>(p, acc, m0, n0, wm, wn,
-                                             SPLIT ? wave * 64 + lane_id_fresh() : tid_v, ring,
-                                             vec, LORA_PRE ? lora_d : nullptr);
+  if constexpr (SPLIT && EPI_OVERLAP) {
+    // The last stage's substep-1 MFMA of block q, issued by the epilogue.
+    auto last_mfma = [&](auto q) {
+      constexpr int nb = q / MB, mb = q % MB;
+      acc[nb][mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+          F[1][MB + nb], F[1][mb], acc[nb][mb], 0, 0, 0, 0, 0, 0);
+    };
+    // The thread index after the loop, recomputed rather than held through it.
+    gemm_epilogue<BM, BN, WGM, WGN, EPI, true>(p, acc, m0, n0, wm, wn,
+                                               wave * 64 + lane_id_fresh(), ring, vec,
+                                               LORA_PRE ? lora_d : nullptr, last_mfma);
+  } else {
+    wait_vmcnt<0, true>();  // every DMA has landed before the ring is reused
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    // The thread index after the loop, recomputed rather than held through it.
+    gemm_epilogue<BM, BN, WGM, WGN, EPI, true>(p, acc, m0, n0, wm, wn,
+                                               SPLIT ? wave * 64 + lane_id_fresh() : tid_v, ring,
+                                               vec, LORA_PRE ? lora_d : nullptr);
+  }
 }
 
 template <int EPI, int BM, int BN, int NS, int PRE, bool SDMA>

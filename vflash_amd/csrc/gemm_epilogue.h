@@ -212,6 +212,12 @@ __device__ __forceinline__ void stage_vectors(const GemmParams& p, int64_t m0, i
   }
 }
 
+// The default `pre` of gemm_epilogue: no MFMA left to issue.
+struct NoPre {
+  template <class Q>
+  __device__ __forceinline__ void operator()(Q) const {}
+};
+
 // Epilogue shared by every tiling, in two phases through LDS.
 //
 // Phase 1 (per wave, from the accumulators): a lane holds, for 32x32 block
@@ -235,12 +241,16 @@ __device__ __forceinline__ void stage_vectors(const GemmParams& p, int64_t m0, i
 // SW_SCALAR: one weight scale for every column (sw[0], the E2M1-weight GEMM's
 // alpha) instead of one per column; a compile-time choice, so the per-value
 // scale needs no select.
-template <int BM, int BN, int WGM, int WGN, int EPI, bool VEC = false, bool SW_SCALAR = false>
+// pre(q): issues the last MFMA of block q = nb * MB + mb (the caller's last
+// K substep), called LAG blocks ahead of phase 1's work on block q, so the
+// MFMA pipe runs those MFMAs under phase 1's VALU work.
+template <int BM, int BN, int WGM, int WGN, int EPI, bool VEC = false, bool SW_SCALAR = false,
+          class Pre = NoPre>
 __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
                                               v16f (&acc)[BN / WGN / 32][BM / WGM / 32],
                                               int64_t m0, int64_t n0, int wm, int wn, int tid,
                                               uint8_t* stage, const uint8_t* vec = nullptr,
-                                              const v16f* lora_d = nullptr) {
+                                              const v16f* lora_d = nullptr, Pre pre = Pre{}) {
   constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
   constexpr int NT = 64 * WGM * WGN;
   constexpr bool LORA = epi_lora(EPI), GATE = epi_gate(EPI), SWIGLU = epi_swiglu(EPI);
@@ -373,8 +383,11 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
       if constexpr (LORA) y = round_bf16_wide(y) + dl;
       return y;
     };
+    constexpr int Q = NB * MB, LAG = 2;
     if constexpr (SWIGLU) {
-      // Value block 2j and gate block 2j + 1 hold the same outputs.
+      // Value block 2j and gate block 2j + 1 hold the same outputs: every
+      // block's last MFMA first.
+      static_for<Q>([&](auto q) { pre(q); });
       const uint32_t* const silu_tab = reinterpret_cast<const uint32_t*>(vec + VEC_LDS);
       static_for<NB / 2>([&](auto j) {
         constexpr int vb = 2 * j, gb = 2 * j + 1;
@@ -419,10 +432,13 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p,
       });
       return;
     }
+    static_for<(LAG < Q ? LAG : Q)>([&](auto q) { pre(q); });
     static_for<NB>([&](auto nb) {
       float sv[4][4], bv[4][4];
       block_vectors(nb, sv, bv);
       static_for<MB>([&](auto mb) {
+        constexpr int q = nb * MB + mb;
+        if constexpr (q + LAG < Q) pre(std::integral_constant<int, q + LAG>{});
         const int row = wm * WM + mb * 32 + fr;  // tile row
         const v16f d = lora_delta(nb, mb);
         static_for<4>([&](auto g) {
