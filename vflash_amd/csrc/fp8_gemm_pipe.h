@@ -35,13 +35,16 @@ namespace vfa {
 // the lds_swizzle chunk permutation.
 //
 // NS = SPLIT_RING selects a split ring instead: two activation slots and three
-// weight slots (160 KB for 256 x 256, 136 KB for 256 x 192).  The weight DMAs of stage kt+2 then go
-// into the slot freed at the barrier of stage kt-1, issued during the first
-// half of stage kt, and only the activation DMAs wait for the barrier of stage
-// kt: the stage's DMA instructions are spread over both halves instead of
-// all crowding the second.  The scale and bias vectors (and the SwiGLU silu
-// table) are DMA'd during the last stage into the third weight slot, which the
-// output staging tile does not cover.
+// weight slots (160 KB for 256 x 256, 136 KB for 256 x 192).  The weight DMAs
+// of stage kt+2 then go into the slot freed at the barrier of stage kt-1,
+// issued during the first half of stage kt, and only the activation DMAs wait
+// for the barrier of stage kt: the stage's DMA instructions are spread over
+// both halves instead of all crowding the second.  The scale and bias vectors
+// (and the SwiGLU silu table) are DMA'd during the last stage into the third
+// weight slot, which the output staging tile does not cover.  With the plain
+// and gate-residual epilogues the last stage ends after its first half: the
+// epilogue issues the substep-1 MFMAs block by block, ahead of its phase-1
+// work on each block, so they run under that VALU work.
 constexpr int SPLIT_RING = 0;
 // Ring bytes of an NS-slot ring (or of the split ring) for a BM x BN tile.
 constexpr int pipe_lds(int bm, int bn, int ns) {
