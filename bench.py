@@ -207,7 +207,8 @@ class EventTimer:
     The kernels run on torch's current stream (the C-ABI is handed
     ``torch.cuda.current_stream()``), so events recorded on that stream bracket
     exactly one launch each.  The events are created before the timed steps
-    (``n`` pairs), so the timed region only records them.
+    (``n`` pairs, each recorded once, since torch creates the HIP event at its
+    first record), so the timed region only records them again.
     """
 
     def __init__(self, n=0):
@@ -215,6 +216,9 @@ class EventTimer:
 
         self.stream = torch.cuda.current_stream()
         self.pool = [self._pair() for _ in range(n)]
+        for s, e in self.pool:
+            s.record(self.stream)
+            e.record(self.stream)
         self.used = 0
 
     @staticmethod
