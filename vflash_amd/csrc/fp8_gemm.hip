@@ -98,15 +98,17 @@ int pick_tiling(int64_t m, int64_t n, int64_t cus, int64_t branch_cols) {
 }
 
 // Tile-order group height.  The 256x256 tiling sweeps four tile rows at a time
-// when the output has at most 48 tile columns (N <= 12288) and two when it has
-// more; the tiles resident on one XCD then share a few A and W panels in that
-// XCD's L2.  Measured at M = 32760: height 4 is 2-5 % faster for N of 3072 to
-// 10240, height 2 is 0.5 % faster for N = 13824 and 1.4 % faster for the
-// SwiGLU projection (112 column tiles).  The other tilings, on grids of one or
-// a few rounds, use eight.
+// when the output has at most 48 tile columns (N <= 12288) and three when it
+// has more; the tiles resident on one XCD then share a few A and W panels in
+// that XCD's L2.  Measured at M = 32760 against heights 2, 3 and 4 in
+// alternating runs: height 4 is the fastest or within 0.3 % for N of 3072 to
+// 10240 and the FFN down projection (height 3 up to 2.5 % slower there);
+// height 3 is 0.5-0.8 % faster than 2 at N = 13824 and 15360 and 2.5-3 % at
+// N = 28672 and the SwiGLU projection (112 column tiles).  The other tilings,
+// on grids of one or a few rounds, use eight.
 int tiling_group_m(int tiling, int64_t tile_cols) {
   if (tiling != GEMM_256x256) return 8;
-  return tile_cols <= 48 ? 4 : 2;
+  return tile_cols <= 48 ? 4 : 3;
 }
 
 // GemmParams::group_m is set here from the tiling.
