@@ -5,6 +5,7 @@ import pytest
 import torch
 
 from oracle import fp8 as O
+from oracle import fp8_torch as T
 from tests.conftest import golden, rel_check, rel_check_device
 from vflash_amd import kernels
 from vflash_amd.fp8_linear import RowFP8Execution, RowFP8Linear
@@ -95,6 +96,15 @@ def test_edges_under_every_tiling(dev, m, k, n, tiles):
     out = kernels.fp8_gemm(a, sa, codes_d, scale_d, m, None)
     got = out.float().cpu().numpy()
     rel_check(got if rows is None else got[rows], oracle_linear(x, codes, scale, None, rows))
+    # The gate-residual epilogue under the same tiling (one K stage, K tails, partial
+    # tiles), on the kernel's own projection: bf16(residual + bf16(gate * y)) exactly.
+    g = torch.Generator().manual_seed(m + n)
+    gate = torch.rand(n, generator=g).to(torch.bfloat16).to(dev)
+    res = torch.randn((m, n), generator=g).to(torch.bfloat16).to(dev)
+    y = kernels.fp8_gemm(a, sa, codes_d, scale_d, m, b.to(dev))
+    gated = kernels.fp8_gemm_gate_residual(a, sa, codes_d, scale_d, m, gate, res, b.to(dev))
+    want = T.gate_residual(res, gate.reshape(1, n).expand(m, n), y).to(torch.bfloat16)
+    assert torch.equal(gated, want)
 
 
 def test_three_dimensional_input_and_torch_quantizer(dev):
