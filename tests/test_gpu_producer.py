@@ -97,6 +97,82 @@ def test_table_rows_gathered_in_place_equal_the_materialized_gather(dev):
         assert torch.equal(q32.codes.view(torch.uint8), q.codes.view(torch.uint8))
 
 
+def run_index(s, r, runs, seed):
+    # Token runs of one modulation row each (a packed sequence groups its tokens by
+    # modality and frame), with run lengths that are not multiples of four.
+    g = torch.Generator().manual_seed(seed)
+    cuts = torch.sort(torch.randperm(s - 1, generator=g)[: runs - 1] + 1).values.tolist()
+    index = torch.empty(s, dtype=torch.int64)
+    for i, (a, b) in enumerate(zip([0] + cuts, cuts + [s])):
+        index[a:b] = (7 * i + 3) % r
+    return index
+
+
+@pytest.mark.parametrize("h,weighted", [(5376, True), (1536, False), (5456, True), (5464, True)])
+def test_index_runs_share_the_modulation_row(dev, h, weighted):
+    # Workgroups whose four rows share a modulation row widen it once (in LDS); the
+    # others, and widths past the shared table, take the per-row path.  Both give
+    # the materialized gather's bits (which runs row by row).
+    b, s, r = 2, 301, 24
+    g = torch.Generator().manual_seed(h)
+    x, w, _, _ = block_input(b, s, h, seed=h + 1)
+    w = w if weighted else None
+    table = (torch.randn((r, 6, h), generator=g) * 0.5).to(torch.bfloat16)
+    index = run_index(s, r, 9, seed=h + 2)
+    d = lambda t: None if t is None else t.to(dev)
+    tb = table.to(dev)
+    scale, shift = tb[:, 1, :], tb[:, 0, :]
+    q = rmsnorm_modulate_quantize(d(x), d(w), scale, shift, eps=1e-6, index=d(index), keep_values=True)
+    gathered = [t.index_select(0, d(index)).contiguous() for t in (scale, shift)]
+    p = rmsnorm_modulate_quantize(d(x), d(w), *gathered, eps=1e-6, keep_values=True)
+    assert torch.equal(q.values, p.values)
+    assert torch.equal(q.codes.view(torch.uint8), p.codes.view(torch.uint8))
+    assert torch.equal(q.scales, p.scales)
+    got = q.values.float().cpu().numpy().reshape(-1, h)
+    ref = oracle_values(x, w, table[:, 1, :], table[:, 0, :], 1e-6, index.numpy()[np.arange(b * s) % s])
+    err = np.abs(got.astype(np.float64) - ref)
+    assert np.all(err <= np.abs(ref) * 2.0**-6 + 2.0**-6 * float(table[:, 0, :].float().abs().max()))
+    assert (got != ref).mean() < 1e-3
+    check_codes(q, got, b * s)
+
+
+def test_one_token_broadcast_shares_the_row(dev):
+    # One modulation row for every row (tokens = 1): the shared path in every full
+    # workgroup, the per-row path in the last (m % 4 rows), equal to the same row
+    # repeated per token.
+    m, h = 1023, 5120
+    x, w, scale, shift = block_input(m, 1, h, seed=41)  # x [m, 1, h], one token
+    d = lambda t: t.to(dev)
+    q = rmsnorm_modulate_quantize(d(x), d(w), d(scale), d(shift), eps=1e-6, keep_values=True)
+    p = rmsnorm_modulate_quantize(d(x).view(1, m, h), d(w), d(scale.expand(m, h).contiguous()),
+                                  d(shift.expand(m, h).contiguous()), eps=1e-6, keep_values=True)
+    assert torch.equal(q.values.view(m, h), p.values.view(m, h))
+    assert torch.equal(q.codes.view(torch.uint8), p.codes.view(torch.uint8))
+    assert torch.equal(q.scales, p.scales)
+    check_codes(q, q.values.float().cpu().numpy().reshape(-1, h), m)
+
+
+def test_a_run_of_indices_outside_the_table_stays_nan(dev):
+    # Four rows with one shared index that lies outside the table: no shared
+    # widening of a row that does not exist; the rows get NaN scales.
+    s, h, r = 16, 512, 4
+    x, w, _, _ = block_input(1, s, h, seed=43)
+    table = torch.randn((r, 6, h)).to(torch.bfloat16).to(dev)
+    index = torch.tensor([1] * 4 + [7] * 4 + [2] * 4 + [-3] * 4, device=dev)
+    q = rmsnorm_modulate_quantize(x.to(dev), w.to(dev), table[:, 1, :], table[:, 0, :], eps=1e-6,
+                                  index=index, keep_values=True)
+    sc = q.scales.reshape(-1).cpu()
+    assert torch.isnan(sc[4:8]).all() and torch.isnan(sc[12:16]).all()
+    assert torch.isfinite(sc[0:4]).all() and torch.isfinite(sc[8:12]).all()
+    # The valid runs against the materialized gather (the per-row path).
+    good = torch.tensor([1] * 4 + [0] * 4 + [2] * 4 + [0] * 4, device=dev)
+    gathered = [t.index_select(0, good).contiguous() for t in (table[:, 1, :], table[:, 0, :])]
+    p = rmsnorm_modulate_quantize(x.to(dev), w.to(dev), *gathered, eps=1e-6, keep_values=True)
+    for rows in (slice(0, 4), slice(8, 12)):
+        assert torch.equal(q.values[0, rows], p.values[0, rows])
+        assert torch.equal(q.codes.view(torch.uint8)[rows], p.codes.view(torch.uint8)[rows])
+
+
 def test_modulation_row_offset_beyond_two_to_the_31_elements(dev):
     # Row 66577 of a [66578, 6, 5376] table starts at element 66577 * 32256 > 2^31 - 1
     # (the strided views of h3_fused_ops.py:24-40).
@@ -166,14 +242,16 @@ def test_consumers_take_the_rows_in_place_of_the_bf16_activation(dev):
     rel_check(out, ref)
 
 
-def test_metric_shape_sampled(dev):
-    # M = 32760 tokens, hidden 5120, modulation rows from a 24-row table.
+@pytest.mark.parametrize("runs", [False, True])
+def test_metric_shape_sampled(dev, runs):
+    # M = 32760 tokens, hidden 5120, modulation rows from a 24-row table: random
+    # per token, or in 24 runs (the shared-row path).
     s, h, r = 32760, 5120, 24
     g = torch.Generator().manual_seed(31)
     x = (torch.randn((1, s, h), generator=g) * 2).to(torch.bfloat16)
     w = (torch.rand(h, generator=g) * 2).to(torch.bfloat16)
     table = (torch.randn((r, 6, h), generator=g) * 0.5).to(torch.bfloat16)
-    index = torch.randint(0, r, (s,), generator=g)
+    index = run_index(s, r, 24, seed=32) if runs else torch.randint(0, r, (s,), generator=g)
     tb = table.to(dev)
     q = rmsnorm_modulate_quantize(x.to(dev), w.to(dev), tb[:, 1, :], tb[:, 0, :], eps=1e-6,
                                   index=index.to(dev), keep_values=True)
