@@ -247,6 +247,31 @@ def test_nvfp4_refusals_count_nothing(value, match):
     assert (ex.calls, ex.rows) == (0, 0)
 
 
+@pytest.mark.parametrize("fmt", ["w4a8", "w4a4"])
+def test_nvfp4_kernel_wrappers_refuse_mismatched_block_scales(fmt):
+    # The kernels address the block scales from N and K alone, so a scale matrix
+    # of another shape is refused before any launch (and before the device check).
+    from vflash_amd import kernels
+
+    n, k, rows = 128, 128, 16
+    packed = torch.zeros((n, k // 2), dtype=torch.uint8)
+    bad_scales = torch.zeros((n, k // 32), dtype=torch.uint8)
+    alpha = torch.tensor([1.0])
+    with pytest.raises(ValueError, match="block scales"):
+        if fmt == "w4a8":
+            codes = torch.zeros((rows, k), dtype=torch.float8_e4m3fn)
+            kernels.nvfp4_gemm(codes, torch.ones(rows, 1), packed, bad_scales, alpha, rows)
+        else:
+            codes = torch.zeros((rows, k // 2), dtype=torch.uint8)
+            act = torch.zeros((128, k // 16), dtype=torch.uint8)
+            kernels.nvfp4_w4a4_gemm(codes, act, packed, bad_scales, alpha, rows)
+    with pytest.raises(ValueError, match="packed weights"):
+        if fmt == "w4a8":
+            kernels.nvfp4_gemm(codes, torch.ones(rows, 1), packed.t(), bad_scales, alpha, rows)
+        else:
+            kernels.nvfp4_w4a4_gemm(codes, act, packed.t(), bad_scales, alpha, rows)
+
+
 # --- measurement ---------------------------------------------------------------
 
 def test_bench_refuses_more_than_one_gpu():

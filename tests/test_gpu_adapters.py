@@ -398,3 +398,26 @@ def test_swiglu_ffn_adapters_h3_shape(dev):
     out = fp8_ffn(ex, x, cu, su, bu, cd, sd, bd, gate, res, activation="swiglu",
                   up_residual=up_res, down_residual=down_res)
     ffn_stage_checks(ex, ops, up_res, down_res, "swiglu", out)
+
+
+def test_lora_linear_refuses_unsupported_adapters_before_counting(dev):
+    # A rank above the epilogue's 128 or a non-BF16 adapter is refused before the
+    # execution counts the call or launches the quantizer.
+    from vflash_amd.fused import fp8_linear_lora
+
+    g = torch.Generator().manual_seed(71)
+    cw, sw = quantize_weight_rows(torch.randn((256, 128), generator=g) * 0.02)
+    x = torch.randn((32, 128), generator=g).to(torch.bfloat16).to(dev)
+    ex = RowFP8Execution("w8a8", activation_quantizer="triton")
+    cases = [
+        (torch.zeros((129, 128), dtype=torch.bfloat16), torch.zeros((256, 129), dtype=torch.bfloat16), "ranks"),
+        (torch.zeros((16, 128)), torch.zeros((256, 16)), "BF16"),
+    ]
+    for la, lb, match in cases:
+        with pytest.raises(ValueError, match=match):
+            fp8_linear_lora(ex, x, cw.to(dev), sw.to(dev), None, la.to(dev), lb.to(dev))
+    assert ex.calls == {"weight_only": 0, "w8a8": 0}
+    # Strength 0 skips the adapter (the reference hook returns the base result).
+    out = fp8_linear_lora(ex, x, cw.to(dev), sw.to(dev), None, cases[1][0].to(dev),
+                          cases[1][1].to(dev), strength=0.0)
+    assert torch.equal(out, ex.linear(x, cw.to(dev), sw.to(dev), None))

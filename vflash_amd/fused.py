@@ -449,6 +449,11 @@ def fp8_linear_lora(
         raise ValueError("Adapter projection does not match the target model")
     if lora_b.shape != (weight.shape[0], lora_a.shape[0]):
         raise ValueError("Adapter projection does not match the target model")
+    # Refused before any counter moves or kernel runs.
+    if lora_a.dtype != torch.bfloat16 or lora_b.dtype != torch.bfloat16:
+        raise ValueError("the fused adapter epilogue takes BF16 adapters")
+    if not 1 <= lora_a.shape[0] <= kernels.LORA_MAX_RANK:
+        raise ValueError(f"the fused adapter epilogue takes ranks 1..{kernels.LORA_MAX_RANK}")
     if execution.observer is not None and sum(execution.calls.values()) % 200 == 0:
         execution.observer()
     execution.calls["w8a8"] += 1

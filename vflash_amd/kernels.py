@@ -543,10 +543,16 @@ def nvfp4_w4a4_gemm(codes, act_scales, packed, block_scales, alpha, rows, bias=N
         raise ValueError("NVFP4 activation codes must be a 2-D uint8 matrix")
     if packed.dtype != torch.uint8 or block_scales.dtype != torch.uint8 or act_scales.dtype != torch.uint8:
         raise ValueError("NVFP4 codes and block scales must be uint8")
+    if packed.ndim != 2 or not packed.is_contiguous():
+        raise ValueError("NVFP4 packed weights must be a contiguous uint8 [N, K/2] matrix")
     n, half_k = packed.shape
     k = 2 * half_k
     if codes.shape != (rows, half_k):
         raise ValueError("NVFP4 activation width differs from the weight")
+    if block_scales.shape != (n, k // 16) or not block_scales.is_contiguous():
+        raise ValueError("NVFP4 block scales must be a contiguous uint8 [N, K/16] matrix")
+    if block_scales.data_ptr() % 16:
+        block_scales = block_scales.clone()  # the kernel copies scale runs with 16-byte DMA
     if act_scales.shape != ((rows + 127) // 128 * 128, k // 16) or not act_scales.is_contiguous():
         raise ValueError("NVFP4 activation scales must be the padded 128x4 layout")
     if alpha.dtype != torch.float32 or alpha.numel() != 1:
