@@ -108,7 +108,40 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
   const uint32_t s_base_any = (uint32_t)((wave & 1) * k_tiles * 512 + lane * 16);
   const int KT = (int)((p.k + 127) / 128);
 
-  auto issue = [&](int j, int s) {
+  // Full tiles with K % 128 == 0 (FULL) advance K and the row blocks through the
+  // scalar offset, and kill stages past the end by switching to an empty
+  // resource, so a DMA instruction costs no vector instruction; other tiles keep
+  // every offset in the lane offset, where the range check zeroes rows past the
+  // end and chunks past K.
+  const bool full = __builtin_amdgcn_readfirstlane(
+                        (int)(rows_a == 256 && rows_w == 256 && p.k % 128 == 0)) != 0;
+  const __amdgpu_buffer_rsrc_t none = make_rsrc(p.w, 0u);
+  auto issue_s = [&](int j, int s) {
+    const uint32_t slot = (uint32_t)j * FP4_SLOT;
+    const bool live = s < KT;
+    const __amdgpu_buffer_rsrc_t ra_s = live ? ra : none, rw_s = live ? rw : none;
+    const __amdgpu_buffer_rsrc_t rs_s = live ? rs : none, ras_s = live ? ras : none;
+    const uint32_t kb = live ? (uint32_t)s * 128u : 0u, kw = kb / 2;
+    if constexpr (A4) {
+      const uint32_t a4_base = (uint32_t)((wave * 64 + (lane >> 2)) * p.lda + wch * 16);
+      static_for<4>([&](auto i) {
+        lds_dma16_so(ra_s, dst_a + slot + i * 1024, a4_base, i * (uint32_t)(16 * p.lda) + kw);
+      });
+    } else {
+      static_for<8>([&](auto i) {
+        lds_dma16_so(ra_s, dst_a + slot + i * 1024, i % 2 ? a_base1 : a_base0, (i / 2) * a_step + kb);
+      });
+    }
+    static_for<4>([&](auto i) {
+      lds_dma16_so(rw_s, dst_w + slot + i * 1024, w_base, i * w_step + kw);
+    });
+    if (wave < 2) {
+      lds_dma16_so(rs_s, dst_s + slot, s_base_any, live ? (uint32_t)s * 1024u : 0u);
+    } else if constexpr (A4) {
+      lds_dma16_so(ras_s, dst_as + slot, s_base_any, live ? (uint32_t)s * 1024u : 0u);
+    }
+  };
+  auto issue_v = [&](int j, int s) {
     const uint32_t slot = (uint32_t)j * FP4_SLOT;
     const int64_t kb = (int64_t)s * 128;
     const int64_t kw = kb / 2;
@@ -137,6 +170,12 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
     } else if constexpr (A4) {
       lds_dma16(ras, dst_as + slot, (s_base_any + (uint32_t)s * 1024) | kills);
     }
+  };
+  auto issue = [&](int j, int s, auto use_s) {
+    if constexpr (use_s)
+      issue_s(j, s);
+    else
+      issue_v(j, s);
   };
 
   const int fr = lane & 31, fh = lane >> 5;
@@ -242,36 +281,48 @@ __global__ void __launch_bounds__(256) nvfp4_gemm_pipe(const GemmParams p) {
 
   Raw r0, r1;
   stage_vectors<256, 256>(p, m0, n0, wave, lane, __builtin_amdgcn_readfirstlane(lds_addr(vec)));
-  issue(0, 0);
-  issue(1, 1);
-  wait_vmcnt<0, true>();
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-  read_raw(r0, 0, I0{});
-  // Same pending LDS reads on both loop entries (see the W8A8 kernel).
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-  // Software pipeline: cur holds the converted operands of the next MFMA step.
-  Ops cur = convert(r0, I0{});
-  for (int kt = 0; kt < KT; ++kt) {
-    const int j = kt & 1;
-    read_raw(r1, j, I1{});
-    cur = pipelined(cur, r0, I1{});
-    cur = pipelined(cur, r0, I2{});
-    cur = pipelined(cur, r0, I3{});
-    cur = pipelined(cur, r1, I0{});
-    cur = pipelined(cur, r1, I1{});
-    // Stage kt+1 has landed for every wave and stage kt is fully read.
+  auto run = [&](auto use_s) {
+    issue(0, 0, use_s);
+    issue(1, 1, use_s);
     wait_vmcnt<0, true>();
-    asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    issue(j, kt + 2);
-    read_raw(r0, 1 - j, I0{});
-    cur = pipelined(cur, r1, I2{});
-    cur = pipelined(cur, r1, I3{});
-    // Half 0 of stage kt+1 (zeros past the last stage, never multiplied).
-    cur = pipelined(cur, r0, I0{});
-  }
+    read_raw(r0, 0, I0{});
+    // Same pending LDS reads on both loop entries (see the W8A8 kernel).
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    // Software pipeline: cur holds the converted operands of the next MFMA step.
+    Ops cur = convert(r0, I0{});
+    // Stage kt in slot jc (a constant: the loop runs two stages per trip, so
+    // every LDS read address is a loop-invariant register plus an immediate).
+    auto stage = [&](int kt, auto jc) {
+      constexpr int j = jc;
+      read_raw(r1, j, I1{});
+      cur = pipelined(cur, r0, I1{});
+      cur = pipelined(cur, r0, I2{});
+      cur = pipelined(cur, r0, I3{});
+      cur = pipelined(cur, r1, I0{});
+      cur = pipelined(cur, r1, I1{});
+      // Stage kt+1 has landed for every wave and stage kt is fully read.
+      wait_vmcnt<0, true>();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      issue(j, kt + 2, use_s);
+      read_raw(r0, 1 - j, I0{});
+      cur = pipelined(cur, r1, I2{});
+      cur = pipelined(cur, r1, I3{});
+      // Half 0 of stage kt+1 (zeros past the last stage, never multiplied).
+      cur = pipelined(cur, r0, I0{});
+    };
+    for (int kt = 0; kt < KT; kt += 2) {
+      stage(kt, I0{});
+      if (kt + 1 < KT) stage(kt + 1, I1{});
+    }
+  };
+  if (full)
+    run(std::true_type{});
+  else
+    run(std::false_type{});
   wait_vmcnt<0, true>();  // every DMA has landed before the ring becomes the staging tile
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
